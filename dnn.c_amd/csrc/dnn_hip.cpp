@@ -1,0 +1,467 @@
+// dnn_hip.cpp -- the C-ABI device layer (include/dnn_hip.h): HBM mirror of the
+// parameters, KV rings, and the launch of the persistent decode kernel.
+#include <hip/hip_runtime.h>
+#include <algorithm>
+#include <cstdarg>
+#include <cstdio>
+#include <cstring>
+#include <string>
+#include <vector>
+
+#include "../../include/dnn_hip.h"
+#include "decode_kernel.h"
+
+using namespace dnnhip;
+
+namespace {
+
+thread_local std::string g_err;
+
+int fail(int code, const char *fmt, ...) {
+    char buf[512];
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(buf, sizeof buf, fmt, ap);
+    va_end(ap);
+    g_err = buf;
+    return code;
+}
+
+#define HIP_TRY(expr)                                                                  \
+    do {                                                                               \
+        hipError_t e_ = (expr);                                                        \
+        if (e_ != hipSuccess)                                                          \
+            return fail(DNN_HIP_EDEVICE, "%s failed: %s", #expr, hipGetErrorString(e_)); \
+    } while (0)
+
+inline size_t round_up(size_t v, size_t a) { return (v + a - 1) / a * a; }
+
+}  // namespace
+
+struct dnn_hip_model {
+    int V, D, L, H, dk, F, ldD, ldF;
+    int device;
+    char *arena = nullptr;
+    size_t arena_bytes = 0;
+    std::vector<LayerW> layers;      // device pointers
+    LayerW *d_layers = nullptr;
+    float *embed = nullptr, *lm_bias = nullptr, *g_final = nullptr;
+    float eps_final = 1e-5f;
+    std::vector<float> eps;          // 2L+1
+    float *rope_cos = nullptr, *rope_sin = nullptr;
+    int rope_rows = 0;
+    // byte offsets of every device tensor inside the arena, for the uploads
+    struct Off { size_t embed, lm_bias, g_final; std::vector<size_t> l; } off;
+};
+
+struct dnn_hip_session {
+    dnn_hip_model *m;
+    int B, max_seq, nch_cap;
+    hipStream_t stream = nullptr;
+    hipEvent_t ev0 = nullptr, ev1 = nullptr;
+    float *x = nullptr, *q = nullptr, *att = nullptr, *act = nullptr, *kc = nullptr, *vc = nullptr;
+    float *part = nullptr, *amax_v = nullptr;
+    int *amax_i = nullptr, *pos = nullptr, *steps_done = nullptr, *err = nullptr;
+    unsigned *att_cnt = nullptr;
+    unsigned long long *bar = nullptr;
+    int *feed = nullptr, *n_feed = nullptr, *ids = nullptr;
+    size_t feed_cap = 0, ids_cap = 0;
+    float *logits = nullptr;
+    size_t logits_cap = 0;
+    int grid_req = 0, grid = 0, grid_cap = 0;
+    float last_ms = 0.f;
+    std::vector<int> h_pos;
+};
+
+namespace {
+
+enum { P_WQKV, P_BQKV, P_WO, P_BO, P_GA, P_GF, P_WG, P_BG, P_WU, P_BU, P_WD, P_BD, NPL };
+
+// Device layout: every tensor 256-byte aligned inside one arena.
+void plan_layout(dnn_hip_model *m) {
+    size_t o = 0;
+    auto take = [&](size_t floats) { size_t r = o; o = round_up(o + floats * sizeof(float), 256); return r; };
+    const size_t D = m->D, F = m->F, V = m->V, ldD = m->ldD, ldF = m->ldF;
+    m->off.embed = take(V * ldD);
+    m->off.lm_bias = take(V);
+    m->off.g_final = take(ldD);
+    m->off.l.assign((size_t)m->L * NPL, 0);
+    for (int l = 0; l < m->L; l++) {
+        size_t *p = &m->off.l[(size_t)l * NPL];
+        p[P_WQKV] = take(3 * D * ldD);
+        p[P_BQKV] = take(3 * D);
+        p[P_WO] = take(D * ldD);
+        p[P_BO] = take(D);
+        p[P_GA] = take(ldD);
+        p[P_GF] = take(ldD);
+        p[P_WG] = take(2 * F * ldD);   // gate and up rows interleaved
+        p[P_BG] = take(F);
+        p[P_WU] = 0;                   // lives inside P_WG
+        p[P_BU] = take(F);
+        p[P_WD] = take(D * ldF);
+        p[P_BD] = take(D);
+    }
+    m->arena_bytes = o;
+}
+
+// W [K][N] (the reference's [in][out]) -> dst[n*ld + k], zero padding k >= K.
+// dst rows are spaced by row_step*ld floats (2 for the interleaved gate/up pair).
+void transpose_into(float *dst, const float *W, int K, int N, int ld, int row_step) {
+    const int TB = 64;
+    for (int k0 = 0; k0 < K; k0 += TB)
+        for (int n0 = 0; n0 < N; n0 += TB)
+            for (int n = n0; n < std::min(N, n0 + TB); n++) {
+                float *d = dst + (size_t)n * row_step * ld;
+                for (int k = k0; k < std::min(K, k0 + TB); k++) d[k] = W[(size_t)k * N + n];
+            }
+}
+
+int upload(dnn_hip_model *m, const float *const *params, int n_params) {
+    const int need = 1 + NPL * m->L + 2;
+    if (!params || n_params != need)
+        return fail(DNN_HIP_EINVAL, "expected %d parameter pointers, got %d", need, n_params);
+    for (int i = 0; i < need; i++)
+        if (!params[i]) return fail(DNN_HIP_EINVAL, "parameter %d is NULL", i);
+    const int D = m->D, F = m->F, V = m->V, ldD = m->ldD, ldF = m->ldF;
+    std::vector<char> host(m->arena_bytes, 0);
+    auto at = [&](size_t off) { return reinterpret_cast<float *>(host.data() + off); };
+    for (int v = 0; v < V; v++) memcpy(at(m->off.embed) + (size_t)v * ldD, params[0] + (size_t)v * D, sizeof(float) * D);
+    memcpy(at(m->off.lm_bias), params[1 + NPL * m->L + 1], sizeof(float) * V);
+    memcpy(at(m->off.g_final), params[1 + NPL * m->L], sizeof(float) * D);
+    for (int l = 0; l < m->L; l++) {
+        const float *const *p = params + 1 + (size_t)l * NPL;
+        const size_t *o = &m->off.l[(size_t)l * NPL];
+        transpose_into(at(o[P_WQKV]), p[P_WQKV], D, 3 * D, ldD, 1);
+        memcpy(at(o[P_BQKV]), p[P_BQKV], sizeof(float) * 3 * D);
+        transpose_into(at(o[P_WO]), p[P_WO], D, D, ldD, 1);
+        memcpy(at(o[P_BO]), p[P_BO], sizeof(float) * D);
+        memcpy(at(o[P_GA]), p[P_GA], sizeof(float) * D);
+        memcpy(at(o[P_GF]), p[P_GF], sizeof(float) * D);
+        transpose_into(at(o[P_WG]), p[P_WG], D, F, ldD, 2);
+        transpose_into(at(o[P_WG]) + ldD, p[P_WU], D, F, ldD, 2);
+        memcpy(at(o[P_BG]), p[P_BG], sizeof(float) * F);
+        memcpy(at(o[P_BU]), p[P_BU], sizeof(float) * F);
+        transpose_into(at(o[P_WD]), p[P_WD], F, D, ldF, 1);
+        memcpy(at(o[P_BD]), p[P_BD], sizeof(float) * D);
+    }
+    HIP_TRY(hipSetDevice(m->device));
+    HIP_TRY(hipMemcpy(m->arena, host.data(), m->arena_bytes, hipMemcpyHostToDevice));
+    return DNN_HIP_OK;
+}
+
+void free_session_buffers(dnn_hip_session *s) {
+    void *bufs[] = {s->x, s->q, s->att, s->act, s->kc, s->vc, s->part, s->amax_v, s->amax_i, s->pos,
+                    s->steps_done, s->err, s->att_cnt, s->bar, s->feed, s->n_feed, s->ids, s->logits};
+    for (void *p : bufs)
+        if (p) (void)hipFree(p);
+}
+
+template <class T>
+int dalloc(T **p, size_t count) {
+    hipError_t e = hipMalloc(reinterpret_cast<void **>(p), std::max<size_t>(count, 1) * sizeof(T));
+    if (e != hipSuccess) { *p = nullptr; return fail(DNN_HIP_ENOMEM, "hipMalloc(%zu bytes): %s", count * sizeof(T), hipGetErrorString(e)); }
+    return DNN_HIP_OK;
+}
+
+template <class T>
+int grow(T **p, size_t *cap, size_t count) {
+    if (count <= *cap) return DNN_HIP_OK;
+    if (*p) (void)hipFree(*p);
+    *p = nullptr;
+    *cap = 0;
+    int rc = dalloc(p, count);
+    if (rc == DNN_HIP_OK) *cap = count;
+    return rc;
+}
+
+int pick_nb(int B) { return B >= 8 ? 8 : B >= 4 ? 4 : B >= 2 ? 2 : 1; }
+
+}  // namespace
+
+extern "C" {
+
+const char *dnn_hip_last_error(void) { return g_err.c_str(); }
+
+int dnn_hip_init(int device) {
+    int n = 0;
+    HIP_TRY(hipGetDeviceCount(&n));
+    if (device < 0 || device >= n) return fail(DNN_HIP_EINVAL, "device %d of %d", device, n);
+    HIP_TRY(hipSetDevice(device));
+    return DNN_HIP_OK;
+}
+
+int dnn_hip_model_create(int V, int D, int L, int H, int dk, int F, const float *const *params,
+                         int n_params, const float *eps, dnn_hip_model **out) {
+    if (!out) return fail(DNN_HIP_EINVAL, "out is NULL");
+    *out = nullptr;
+    if (V <= 0 || D <= 0 || L <= 0 || H <= 0 || F <= 0 || dk <= 0)
+        return fail(DNN_HIP_EINVAL, "non-positive dimension");
+    if (D != H * dk) return fail(DNN_HIP_EINVAL, "d_model %d != n_heads %d * d_k %d", D, H, dk);
+    if (dk != DK) return fail(DNN_HIP_EINVAL, "the decode kernels are built for d_k=%d (got %d)", DK, dk);
+    if (D % 2 || V % 2) return fail(DNN_HIP_EINVAL, "d_model and vocab_size must be even");
+    int dev = 0;
+    HIP_TRY(hipGetDevice(&dev));
+    auto *m = new dnn_hip_model();
+    m->V = V; m->D = D; m->L = L; m->H = H; m->dk = dk; m->F = F;
+    m->ldD = (int)round_up(D, LDALIGN);
+    m->ldF = (int)round_up(F, LDALIGN);
+    m->device = dev;
+    m->eps.assign(2 * L + 1, 1e-5f);
+    if (eps) for (int i = 0; i < 2 * L + 1; i++) m->eps[i] = eps[i];
+    m->eps_final = m->eps[2 * L];
+    plan_layout(m);
+    hipError_t e = hipMalloc(reinterpret_cast<void **>(&m->arena), m->arena_bytes);
+    if (e != hipSuccess) { delete m; return fail(DNN_HIP_ENOMEM, "hipMalloc(%zu) for weights: %s", m->arena_bytes, hipGetErrorString(e)); }
+    int rc = upload(m, params, n_params);
+    if (rc != DNN_HIP_OK) { (void)hipFree(m->arena); delete m; return rc; }
+    auto dp = [&](size_t off) { return reinterpret_cast<float *>(m->arena + off); };
+    m->embed = dp(m->off.embed);
+    m->lm_bias = dp(m->off.lm_bias);
+    m->g_final = dp(m->off.g_final);
+    m->layers.resize(L);
+    for (int l = 0; l < L; l++) {
+        const size_t *o = &m->off.l[(size_t)l * NPL];
+        LayerW &w = m->layers[l];
+        w.wqkv = dp(o[P_WQKV]); w.bqkv = dp(o[P_BQKV]);
+        w.wo = dp(o[P_WO]); w.bo = dp(o[P_BO]);
+        w.g_attn = dp(o[P_GA]); w.g_ffn = dp(o[P_GF]);
+        w.wgu = dp(o[P_WG]); w.bg = dp(o[P_BG]); w.bu = dp(o[P_BU]);
+        w.wd = dp(o[P_WD]); w.bd = dp(o[P_BD]);
+        w.eps_attn = m->eps[2 * l];
+        w.eps_ffn = m->eps[2 * l + 1];
+    }
+    e = hipMalloc(reinterpret_cast<void **>(&m->d_layers), sizeof(LayerW) * L);
+    if (e == hipSuccess) e = hipMemcpy(m->d_layers, m->layers.data(), sizeof(LayerW) * L, hipMemcpyHostToDevice);
+    if (e != hipSuccess) {
+        (void)hipFree(m->arena);
+        if (m->d_layers) (void)hipFree(m->d_layers);
+        delete m;
+        return fail(DNN_HIP_EDEVICE, "layer table upload: %s", hipGetErrorString(e));
+    }
+    *out = m;
+    return DNN_HIP_OK;
+}
+
+int dnn_hip_model_update(dnn_hip_model *m, const float *const *params, int n_params) {
+    if (!m) return fail(DNN_HIP_EINVAL, "model is NULL");
+    return upload(m, params, n_params);
+}
+
+int dnn_hip_model_rope(dnn_hip_model *m, const float *cos_table, const float *sin_table, int rows) {
+    if (!m) return fail(DNN_HIP_EINVAL, "model is NULL");
+    HIP_TRY(hipSetDevice(m->device));
+    if (m->rope_cos) { (void)hipFree(m->rope_cos); m->rope_cos = nullptr; }
+    if (m->rope_sin) { (void)hipFree(m->rope_sin); m->rope_sin = nullptr; }
+    m->rope_rows = 0;
+    if (!cos_table || !sin_table) return DNN_HIP_OK;
+    if (rows <= 0) return fail(DNN_HIP_EINVAL, "rope rows %d", rows);
+    const size_t n = (size_t)rows * (m->dk / 2);
+    int rc = dalloc(&m->rope_cos, n);
+    if (rc) return rc;
+    rc = dalloc(&m->rope_sin, n);
+    if (rc) return rc;
+    HIP_TRY(hipMemcpy(m->rope_cos, cos_table, n * sizeof(float), hipMemcpyHostToDevice));
+    HIP_TRY(hipMemcpy(m->rope_sin, sin_table, n * sizeof(float), hipMemcpyHostToDevice));
+    m->rope_rows = rows;
+    return DNN_HIP_OK;
+}
+
+int dnn_hip_model_destroy(dnn_hip_model *m) {
+    if (!m) return DNN_HIP_OK;
+    (void)hipSetDevice(m->device);
+    if (m->arena) (void)hipFree(m->arena);
+    if (m->d_layers) (void)hipFree(m->d_layers);
+    if (m->rope_cos) (void)hipFree(m->rope_cos);
+    if (m->rope_sin) (void)hipFree(m->rope_sin);
+    delete m;
+    return DNN_HIP_OK;
+}
+
+int dnn_hip_session_create(dnn_hip_model *m, int B, int max_seq, dnn_hip_session **out) {
+    if (!m || !out) return fail(DNN_HIP_EINVAL, "NULL argument");
+    *out = nullptr;
+    if (B <= 0 || B > MAXB) return fail(DNN_HIP_EINVAL, "batch %d outside [1,%d]", B, MAXB);
+    if (max_seq <= 0) return fail(DNN_HIP_EINVAL, "max_seq %d", max_seq);
+    HIP_TRY(hipSetDevice(m->device));
+    auto *s = new dnn_hip_session();
+    s->m = m;
+    s->B = B;
+    s->max_seq = max_seq;
+    s->nch_cap = (max_seq + CH - 1) / CH;
+    s->h_pos.assign(B, 0);
+    const size_t kv = (size_t)m->L * B * m->H * max_seq * DK;
+    int rc = 0;
+    int dev_cu = 0;
+    if (hipDeviceGetAttribute(&dev_cu, hipDeviceAttributeMultiprocessorCount, m->device) != hipSuccess) dev_cu = 256;
+    s->grid_cap = dev_cu * 8;
+    rc = rc ? rc : dalloc(&s->x, (size_t)B * m->ldD);
+    rc = rc ? rc : dalloc(&s->q, (size_t)B * m->H * DK);
+    rc = rc ? rc : dalloc(&s->att, (size_t)B * m->ldD);
+    rc = rc ? rc : dalloc(&s->act, (size_t)B * m->ldF);
+    rc = rc ? rc : dalloc(&s->kc, kv);
+    rc = rc ? rc : dalloc(&s->vc, kv);
+    rc = rc ? rc : dalloc(&s->part, (size_t)B * m->H * s->nch_cap * (DK + 2));
+    rc = rc ? rc : dalloc(&s->amax_v, (size_t)B * s->grid_cap);
+    rc = rc ? rc : dalloc(&s->amax_i, (size_t)B * s->grid_cap);
+    rc = rc ? rc : dalloc(&s->pos, (size_t)B);
+    rc = rc ? rc : dalloc(&s->steps_done, 1);
+    rc = rc ? rc : dalloc(&s->err, 1);
+    rc = rc ? rc : dalloc(&s->att_cnt, (size_t)B * m->H);
+    rc = rc ? rc : dalloc(&s->bar, 1);
+    rc = rc ? rc : dalloc(&s->n_feed, (size_t)B);
+    if (rc) { free_session_buffers(s); delete s; return rc; }
+    hipError_t e = hipStreamCreateWithFlags(&s->stream, hipStreamNonBlocking);
+    if (e == hipSuccess) e = hipEventCreate(&s->ev0);
+    if (e == hipSuccess) e = hipEventCreate(&s->ev1);
+    // padding lanes of the activation rows must stay zero: they meet zero weights
+    if (e == hipSuccess) e = hipMemset(s->x, 0, sizeof(float) * (size_t)B * m->ldD);
+    if (e == hipSuccess) e = hipMemset(s->att, 0, sizeof(float) * (size_t)B * m->ldD);
+    if (e == hipSuccess) e = hipMemset(s->act, 0, sizeof(float) * (size_t)B * m->ldF);
+    if (e == hipSuccess) e = hipMemset(s->kc, 0, sizeof(float) * kv);
+    if (e == hipSuccess) e = hipMemset(s->vc, 0, sizeof(float) * kv);
+    if (e == hipSuccess) e = hipMemset(s->att_cnt, 0, sizeof(unsigned) * (size_t)B * m->H);
+    if (e == hipSuccess) e = hipMemset(s->pos, 0, sizeof(int) * (size_t)B);
+    if (e != hipSuccess) {
+        free_session_buffers(s);
+        delete s;
+        return fail(DNN_HIP_EDEVICE, "session setup: %s", hipGetErrorString(e));
+    }
+    *out = s;
+    return DNN_HIP_OK;
+}
+
+int dnn_hip_session_reset(dnn_hip_session *s) {
+    if (!s) return fail(DNN_HIP_EINVAL, "session is NULL");
+    HIP_TRY(hipSetDevice(s->m->device));
+    HIP_TRY(hipMemset(s->pos, 0, sizeof(int) * (size_t)s->B));
+    std::fill(s->h_pos.begin(), s->h_pos.end(), 0);
+    return DNN_HIP_OK;
+}
+
+int dnn_hip_session_lengths(dnn_hip_session *s, int *lens) {
+    if (!s || !lens) return fail(DNN_HIP_EINVAL, "NULL argument");
+    memcpy(lens, s->h_pos.data(), sizeof(int) * (size_t)s->B);
+    return DNN_HIP_OK;
+}
+
+int dnn_hip_session_destroy(dnn_hip_session *s) {
+    if (!s) return DNN_HIP_OK;
+    (void)hipSetDevice(s->m->device);
+    if (s->stream) (void)hipStreamSynchronize(s->stream);
+    free_session_buffers(s);
+    if (s->ev0) (void)hipEventDestroy(s->ev0);
+    if (s->ev1) (void)hipEventDestroy(s->ev1);
+    if (s->stream) (void)hipStreamDestroy(s->stream);
+    delete s;
+    return DNN_HIP_OK;
+}
+
+int dnn_hip_session_set_grid(dnn_hip_session *s, int n) {
+    if (!s || n < 0) return fail(DNN_HIP_EINVAL, "bad argument");
+    s->grid_req = n;
+    return DNN_HIP_OK;
+}
+
+int dnn_hip_session_last_ms(dnn_hip_session *s, float *ms) {
+    if (!s || !ms) return fail(DNN_HIP_EINVAL, "NULL argument");
+    *ms = s->last_ms;
+    return DNN_HIP_OK;
+}
+
+int dnn_hip_decode(dnn_hip_session *s, const int *feed, int n_feed_all, const int *n_feed,
+                   int n_steps, int eos, int *ids, float *logits, int *steps_done) {
+    if (!s || !feed) return fail(DNN_HIP_EINVAL, "NULL argument");
+    dnn_hip_model *m = s->m;
+    const int B = s->B;
+    if (n_steps <= 0) return fail(DNN_HIP_EINVAL, "n_steps %d", n_steps);
+    std::vector<int> nf(B);
+    int nf_max = 0;
+    for (int b = 0; b < B; b++) {
+        nf[b] = n_feed ? n_feed[b] : n_feed_all;
+        if (nf[b] < 1) return fail(DNN_HIP_EINVAL, "row %d: n_feed %d < 1", b, nf[b]);
+        nf_max = std::max(nf_max, nf[b]);
+    }
+    for (int t = 0; t < nf_max; t++)
+        for (int b = 0; b < B; b++)
+            if (t < nf[b] && (feed[(size_t)t * B + b] < 0 || feed[(size_t)t * B + b] >= m->V))
+                return fail(DNN_HIP_ERANGE, "token id %d at step %d row %d outside [0,%d)",
+                            feed[(size_t)t * B + b], t, b, m->V);
+    for (int b = 0; b < B; b++) {
+        if (s->h_pos[b] + n_steps > s->max_seq)
+            return fail(DNN_HIP_ERANGE, "row %d: %d cached + %d steps exceeds max_seq %d", b, s->h_pos[b], n_steps, s->max_seq);
+        if (m->rope_cos && s->h_pos[b] + n_steps > m->rope_rows)
+            return fail(DNN_HIP_ERANGE, "row %d: position %d beyond the RoPE table (%d rows)", b, s->h_pos[b] + n_steps - 1, m->rope_rows);
+    }
+    HIP_TRY(hipSetDevice(m->device));
+    int rc = grow(&s->feed, &s->feed_cap, (size_t)nf_max * B);
+    if (!rc) rc = grow(&s->ids, &s->ids_cap, (size_t)n_steps * B);
+    if (!rc && logits) rc = grow(&s->logits, &s->logits_cap, (size_t)n_steps * B * m->V);
+    if (rc) return rc;
+    HIP_TRY(hipMemcpyAsync(s->feed, feed, sizeof(int) * (size_t)nf_max * B, hipMemcpyHostToDevice, s->stream));
+    HIP_TRY(hipMemcpyAsync(s->n_feed, nf.data(), sizeof(int) * B, hipMemcpyHostToDevice, s->stream));
+    HIP_TRY(hipMemsetAsync(s->bar, 0, sizeof(unsigned long long), s->stream));
+    HIP_TRY(hipMemsetAsync(s->err, 0, sizeof(int), s->stream));
+
+    const int nb = pick_nb(B);
+    const void *kern = decode_kernel_for(nb);
+    const size_t shmem = lds_bytes(nb, std::max(m->ldD, m->ldF));
+    HIP_TRY(hipFuncSetAttribute(kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)shmem));
+    int per_cu = 0, n_cu = 0;
+    HIP_TRY(hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kern, BLOCK, shmem));
+    HIP_TRY(hipDeviceGetAttribute(&n_cu, hipDeviceAttributeMultiprocessorCount, m->device));
+    int grid = per_cu * n_cu;
+    if (s->grid_req > 0) grid = std::min(grid, s->grid_req);
+    grid = std::min(grid, s->grid_cap);
+    if (grid <= 0) return fail(DNN_HIP_EDEVICE, "decode kernel does not fit on a CU (shmem %zu)", shmem);
+    s->grid = grid;
+
+    DecodeArgs a{};
+    a.V = m->V; a.D = m->D; a.L = m->L; a.H = m->H; a.F = m->F; a.ldD = m->ldD; a.ldF = m->ldF;
+    a.layers = m->d_layers;
+    a.embed = m->embed; a.lm_bias = m->lm_bias; a.g_final = m->g_final; a.eps_final = m->eps_final;
+    a.rope_cos = m->rope_cos; a.rope_sin = m->rope_sin;
+    a.B = B; a.max_seq = s->max_seq; a.nch_cap = s->nch_cap;
+    a.x = s->x; a.q = s->q; a.att = s->att; a.act = s->act; a.kc = s->kc; a.vc = s->vc;
+    a.pos = s->pos; a.part = s->part; a.att_cnt = s->att_cnt; a.amax_v = s->amax_v; a.amax_i = s->amax_i;
+    a.feed = s->feed; a.n_feed = s->n_feed; a.ids = s->ids; a.logits = logits ? s->logits : nullptr;
+    a.n_steps = n_steps; a.eos = eos; a.bar = s->bar; a.err = s->err; a.steps_done = s->steps_done;
+    void *kargs[] = {&a};
+    HIP_TRY(hipEventRecord(s->ev0, s->stream));
+    HIP_TRY(hipLaunchCooperativeKernel(kern, dim3(grid), dim3(BLOCK), kargs, (unsigned)shmem, s->stream));
+    HIP_TRY(hipEventRecord(s->ev1, s->stream));
+    HIP_TRY(hipEventSynchronize(s->ev1));
+    HIP_TRY(hipEventElapsedTime(&s->last_ms, s->ev0, s->ev1));
+    int done = 0, kerr = 0;
+    HIP_TRY(hipMemcpy(&kerr, s->err, sizeof(int), hipMemcpyDeviceToHost));
+    if (kerr) return fail(DNN_HIP_EDEVICE, "decode kernel: a grid barrier timed out (error bits %#x); results discarded", kerr);
+    HIP_TRY(hipMemcpy(&done, s->steps_done, sizeof(int), hipMemcpyDeviceToHost));
+    if (ids) HIP_TRY(hipMemcpy(ids, s->ids, sizeof(int) * (size_t)done * B, hipMemcpyDeviceToHost));
+    if (logits) HIP_TRY(hipMemcpy(logits, s->logits, sizeof(float) * (size_t)done * B * m->V, hipMemcpyDeviceToHost));
+    HIP_TRY(hipMemcpy(s->h_pos.data(), s->pos, sizeof(int) * B, hipMemcpyDeviceToHost));
+    if (steps_done) *steps_done = done;
+    return DNN_HIP_OK;
+}
+
+int dnn_hip_generate(dnn_hip_model *m, const int *prompt, int P, int max_new, int eos, int *out, int *n_out) {
+    if (!m || !prompt || !out || !n_out) return fail(DNN_HIP_EINVAL, "NULL argument");
+    if (P <= 0 || max_new <= 0) return fail(DNN_HIP_EINVAL, "prompt %d / max_new %d", P, max_new);
+    dnn_hip_session *s = nullptr;
+    int rc = dnn_hip_session_create(m, 1, P + max_new, &s);
+    if (rc) return rc;
+    const int steps = P + max_new - 1;
+    std::vector<int> ids(steps);
+    int done = 0;
+    rc = dnn_hip_decode(s, prompt, P, nullptr, steps, eos, ids.data(), nullptr, &done);
+    dnn_hip_session_destroy(s);
+    if (rc) return rc;
+    if (out != prompt) memmove(out, prompt, sizeof(int) * P);
+    int n = P;
+    for (int t = P - 1; t < done; t++) {
+        out[n++] = ids[t];
+        if (eos >= 0 && ids[t] == eos) break;
+    }
+    *n_out = n;
+    return DNN_HIP_OK;
+}
+
+}  // extern "C"

@@ -1,0 +1,124 @@
+/* device.c -- maps each decoder_lm to its HBM mirror (dnn_hip_model).
+ *
+ * The decoder_lm struct is the reference's and has no room for a device
+ * handle, so mirrors live in a small table keyed by the model pointer.  A
+ * mirror is refreshed when a fingerprint of the host parameters changes: the
+ * parameter pointers and shapes, 64 evenly spaced values of every tensor, and
+ * the RoPE table pointers.  Training or module_load rewrite whole tensors and
+ * change it; decoder_lm_device_sync covers edits the samples could miss. */
+#include "device.h"
+#include <assert.h>
+#include <stdint.h>
+#include <stdio.h>
+#include <stdlib.h>
+#include <string.h>
+
+#define MAX_MIRRORS 64
+
+typedef struct {
+    decoder_lm *lm;
+    dnn_hip_model *dm;
+    uint64_t print;
+} mirror;
+
+static mirror g_mirrors[MAX_MIRRORS];
+static int g_device_ready;
+
+void dnn_amd_check(int rc, const char *what) {
+    if (rc != DNN_HIP_OK) fprintf(stderr, "dnn_amd: %s failed (%d): %s\n", what, rc, dnn_hip_last_error());
+    assert(rc == DNN_HIP_OK && "device call failed");
+}
+
+static uint64_t mix(uint64_t h, uint64_t v) {
+    h ^= v;
+    return h * 1099511628211ULL;
+}
+
+static uint64_t fingerprint(decoder_lm *lm) {
+    int n;
+    tensor **ps = module_parameters(&lm->base, &n);
+    uint64_t h = 1469598103934665603ULL;
+    for (int i = 0; i < n; i++) {
+        const int ne = tensor_numel(ps[i]);
+        const float *d = tensor_data_ptr(ps[i]);
+        h = mix(h, (uint64_t)(uintptr_t)d);
+        h = mix(h, (uint64_t)ne);
+        for (int k = 0; k < 64; k++) {
+            uint32_t bits;
+            memcpy(&bits, &d[(long long)k * ne / 64], 4);
+            h = mix(h, bits);
+        }
+    }
+    tensor *fc = lm->blocks[0]->freqs_cos;
+    h = mix(h, (uint64_t)(uintptr_t)fc);
+    h = mix(h, fc ? (uint64_t)fc->shape[0] : 0);
+    return h;
+}
+
+static void params_of(decoder_lm *lm, const float **ptrs, int *n_out, float *eps) {
+    int n;
+    tensor **ps = module_parameters(&lm->base, &n);
+    assert(n == 1 + 12 * lm->n_layers + 2 && "decoder_lm: unexpected parameter count");
+    for (int i = 0; i < n; i++) ptrs[i] = tensor_data_ptr(ps[i]);
+    for (int l = 0; l < lm->n_layers; l++) {
+        eps[2 * l] = lm->blocks[l]->attn_norm->eps;
+        eps[2 * l + 1] = lm->blocks[l]->ffn_norm->eps;
+    }
+    eps[2 * lm->n_layers] = lm->norm->eps;
+    *n_out = n;
+}
+
+static void upload_rope(decoder_lm *lm, dnn_hip_model *dm) {
+    tensor *c = lm->blocks[0]->freqs_cos, *s = lm->blocks[0]->freqs_sin;
+    if (c && s) dnn_amd_check(dnn_hip_model_rope(dm, tensor_data_ptr(c), tensor_data_ptr(s), c->shape[0]), "dnn_hip_model_rope");
+    else dnn_amd_check(dnn_hip_model_rope(dm, NULL, NULL, 0), "dnn_hip_model_rope");
+}
+
+static mirror *find(decoder_lm *lm) {
+    for (int i = 0; i < MAX_MIRRORS; i++)
+        if (g_mirrors[i].lm == lm) return &g_mirrors[i];
+    return NULL;
+}
+
+dnn_hip_model *dnn_amd_device_model(decoder_lm *lm) {
+    if (!g_device_ready) { dnn_amd_check(dnn_hip_init(0), "dnn_hip_init"); g_device_ready = 1; }
+    const int np = 1 + 12 * lm->n_layers + 2;
+    const float **ptrs = malloc(sizeof(float *) * (size_t)np);
+    float *eps = malloc(sizeof(float) * (size_t)(2 * lm->n_layers + 1));
+    int n;
+    params_of(lm, ptrs, &n, eps);
+    const uint64_t fp = fingerprint(lm);
+    mirror *m = find(lm);
+    if (!m) {
+        m = find(NULL);
+        assert(m && "dnn_amd: too many device mirrors; release some with decoder_lm_device_release");
+        const transformer_block *b = lm->blocks[0];
+        dnn_amd_check(dnn_hip_model_create(lm->vocab_size, lm->d_model, lm->n_layers, b->n_heads, b->d_k,
+                                           b->ffn->intermediate_size, ptrs, n, eps, &m->dm),
+                      "dnn_hip_model_create");
+        m->lm = lm;
+        upload_rope(lm, m->dm);
+        m->print = fp;
+    } else if (m->print != fp) {
+        dnn_amd_check(dnn_hip_model_update(m->dm, ptrs, n), "dnn_hip_model_update");
+        upload_rope(lm, m->dm);
+        m->print = fp;
+    }
+    free(ptrs);
+    free(eps);
+    return m->dm;
+}
+
+void decoder_lm_device_sync(decoder_lm *lm) {
+    mirror *m = find(lm);
+    if (m) m->print = 0;
+    (void)dnn_amd_device_model(lm);
+}
+
+void decoder_lm_device_release(decoder_lm *lm) {
+    mirror *m = find(lm);
+    if (!m) return;
+    dnn_hip_model_destroy(m->dm);
+    m->lm = NULL;
+    m->dm = NULL;
+}

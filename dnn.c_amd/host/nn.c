@@ -1,0 +1,63 @@
+/* nn.c -- layer construction for the decode path (reference src/nn.c:10-25,
+ * 40-59, 152-167, 177-191).  Creation order and bounds are the reference's, so
+ * the same dnn_seed() yields the same weights. */
+#include "dnn/nn.h"
+#include <assert.h>
+#include <math.h>
+
+linear *linear_create(struct mem_pool *params, int in_features, int out_features) {
+    assert(in_features > 0 && out_features > 0);
+    linear *l = _mem_pool_alloc(params, sizeof(linear), NULL);
+    module_init(&l->base, params, "linear");
+    l->in_features = in_features;
+    l->out_features = out_features;
+    const float bound = 1.0f / sqrtf((float)in_features);
+    l->weight = tensor_uniform(params, 2, (int[]){in_features, out_features}, 1, bound);
+    l->bias = tensor_uniform(params, 1, (int[]){out_features}, 1, bound);
+    module_param(&l->base, "weight", l->weight);
+    module_param(&l->base, "bias", l->bias);
+    return l;
+}
+
+swiglu_ffn *swiglu_ffn_create(struct mem_pool *params, int d_model, int intermediate_size) {
+    assert(d_model > 0 && intermediate_size > 0);
+    swiglu_ffn *f = _mem_pool_alloc(params, sizeof(swiglu_ffn), NULL);
+    module_init(&f->base, params, "swiglu_ffn");
+    f->d_model = d_model;
+    f->intermediate_size = intermediate_size;
+    f->gate_proj = linear_create(params, d_model, intermediate_size);
+    module_add_child(&f->base, "gate_proj", &f->gate_proj->base);
+    f->up_proj = linear_create(params, d_model, intermediate_size);
+    module_add_child(&f->base, "up_proj", &f->up_proj->base);
+    f->down_proj = linear_create(params, intermediate_size, d_model);
+    module_add_child(&f->base, "down_proj", &f->down_proj->base);
+    return f;
+}
+
+rms_norm *rms_norm_create(struct mem_pool *params, int d, float eps) {
+    assert(d > 0);
+    rms_norm *r = _mem_pool_alloc(params, sizeof(rms_norm), NULL);
+    module_init(&r->base, params, "rms_norm");
+    r->d = d;
+    r->eps = eps;
+    r->weight = tensor_zeros(params, 1, (int[]){d}, 1);
+    float *w = tensor_data_ptr(r->weight);
+    for (int i = 0; i < d; i++) w[i] = 1.0f;
+    module_param(&r->base, "weight", r->weight);
+    return r;
+}
+
+embedding *embedding_create(struct mem_pool *params, int vocab_size, int d_model) {
+    assert(vocab_size > 0 && d_model > 0);
+    embedding *e = _mem_pool_alloc(params, sizeof(embedding), NULL);
+    module_init(&e->base, params, "embedding");
+    e->vocab_size = vocab_size;
+    e->d_model = d_model;
+    e->weight = tensor_uniform(params, 2, (int[]){vocab_size, d_model}, 1, 1.0f / sqrtf((float)d_model));
+    module_param(&e->base, "weight", e->weight);
+    return e;
+}
+
+long long linear_num_parameters(linear *l) { return module_num_parameters(&l->base); }
+long long swiglu_ffn_num_parameters(swiglu_ffn *f) { return module_num_parameters(&f->base); }
+long long embedding_num_parameters(embedding *e) { return module_num_parameters(&e->base); }

@@ -1,0 +1,46 @@
+/* gpt.h -- decoder-only LM (reference include/gpt.h:20-118): construction,
+ * initialisation, RoPE, and the generation loop, which runs on the MI355X
+ * through include/dnn_hip.h.  The training step of the reference is not part
+ * of this library. */
+#ifndef DNN_GPT_H
+#define DNN_GPT_H
+#include "tensor.h"
+#include "module.h"
+#include "nn.h"
+#include "transformer.h"
+
+typedef struct {
+    module               base;
+    embedding           *embed;
+    transformer_block  **blocks;
+    int                  n_layers;
+    rms_norm            *norm;
+    linear              *lm_head;     /* weight NULL: tied to embed->weight */
+    int                  d_model;
+    int                  vocab_size;
+} decoder_lm;
+
+decoder_lm *decoder_lm_create(struct mem_pool *params_pool, int vocab_size, int d_model,
+                              int n_layers, int n_heads, int d_k, int intermediate_size);
+void        decoder_lm_init_weights(decoder_lm *lm);
+void        decoder_lm_enable_rope(struct mem_pool *params_pool, decoder_lm *lm, int max_seq_len, float base);
+long long   decoder_lm_num_parameters(decoder_lm *lm);
+
+int decoder_lm_argmax_token(const float *logits, int vocab_size);
+int decoder_lm_sample_with_temp(const float *logits, int vocab_size, float temp);
+
+/* Greedy (temperature 0) or sampled generation.  prompt_ids [1, N] int32.
+ * Returns prompt + generated ids from data_pool; *n_out = their count. */
+int *decoder_lm_generate(struct mem_pool *scratch_pool, struct mem_pool *data_pool,
+                         decoder_lm *lm, const tensor *prompt_ids,
+                         int max_new_tokens, float temperature, int use_cache, int *n_out);
+
+/* ---- device mirror control (no counterpart in the reference) ----
+ * The first generate call mirrors the parameters into HBM; later calls
+ * re-upload when the sampled fingerprint of the host weights changed.
+ * decoder_lm_device_sync forces a re-upload (e.g. after editing a few
+ * weights in place); decoder_lm_device_release frees the mirror. */
+void decoder_lm_device_sync(decoder_lm *lm);
+void decoder_lm_device_release(decoder_lm *lm);
+
+#endif

@@ -1,0 +1,39 @@
+/* transformer.h -- KV cache and pre-norm block (reference include/transformer.h:26-131). */
+#ifndef DNN_TRANSFORMER_H
+#define DNN_TRANSFORMER_H
+#include "tensor.h"
+#include "module.h"
+#include "nn.h"
+#include "attention.h"
+
+typedef struct {
+    tensor *k_cache;   /* [B, H, max_seq, d_k] */
+    tensor *v_cache;   /* [B, H, max_seq, d_k] */
+    int     seq_len;
+    int     max_seq;
+} kv_cache;
+
+kv_cache *kv_cache_create(struct mem_pool *params_pool, int B, int H, int max_seq, int d_k);
+void      kv_cache_append(kv_cache *kvc, const tensor *K_new, const tensor *V_new);
+tensor   *kv_cache_get_K(struct mem_pool *scratch, kv_cache *kvc);
+tensor   *kv_cache_get_V(struct mem_pool *scratch, kv_cache *kvc);
+
+typedef struct {
+    module      base;
+    linear     *qkv_proj;
+    linear     *out_proj;
+    int         n_heads;
+    int         d_k;
+    int         d_model;
+    rms_norm   *attn_norm;
+    rms_norm   *ffn_norm;
+    swiglu_ffn *ffn;
+    tensor     *freqs_cos;   /* [max_seq_len, d_k/2] or NULL */
+    tensor     *freqs_sin;
+} transformer_block;
+
+transformer_block *transformer_block_create(struct mem_pool *params_pool, int d_model, int n_heads,
+                                            int d_k, int intermediate_size);
+long long transformer_block_num_parameters(transformer_block *block);
+
+#endif

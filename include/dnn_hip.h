@@ -1,0 +1,123 @@
+/*
+ * dnn_hip.h -- the C-ABI device layer of the MI355X (gfx950) decode path.
+ *
+ * Plain C: opaque handles, plain pointers and sizes, int status codes.  The host
+ * library (libdnn_amd.so, the reference-compatible API declared in include/dnn/)
+ * calls these; so can any FFI (ctypes, cgo, JNI) directly.
+ *
+ * Which reference interface each entry point serves:
+ *   dnn_hip_model_create  <- the params pool as built by decoder_lm_create
+ *                            (gpt.c:16-62) and filled by init/module_load; the
+ *                            pointers are module_parameters() order (module.c:123-142)
+ *   dnn_hip_model_rope    <- decoder_lm_enable_rope / tensor_rope_freqs_init
+ *                            (gpt.c:481-496, rope.c:148-171)
+ *   dnn_hip_session_*     <- kv_cache_create / the per-layer caches of
+ *                            decoder_lm_generate (transformer.c:30-38, gpt.c:295-301),
+ *                            extended with one sequence length per batch row
+ *                            (the seq_lens convention of attention.h:39-41)
+ *   dnn_hip_decode        <- the token loop of decoder_lm_generate (gpt.c:306-375):
+ *                            embedding -> transformer_block_forward_cached x L
+ *                            (transformer.c:211-416) -> final rms_norm -> tied
+ *                            lm_head (gpt.c:117-122) -> argmax (gpt.c:220-230)
+ *   dnn_hip_generate      <- decoder_lm_generate(use_cache=1, temperature=0)
+ *                            (gpt.h:104-108)
+ *
+ * Errors: every call returns DNN_HIP_OK (0) or a negative code; the message of
+ * the last failure on the calling thread is dnn_hip_last_error().  The
+ * reference asserts on the same conditions (pool.c:39-40, transformer.c:55-56,
+ * embedding.c:82, gpt.c:264); the host library turns a non-zero code into the
+ * same fatal assert.
+ *
+ * Threading: a model or session is used by one host thread at a time.  All
+ * calls are synchronous: results are in host memory when they return.
+ */
+#ifndef DNN_HIP_H
+#define DNN_HIP_H
+
+#include <stddef.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define DNN_HIP_OK        0
+#define DNN_HIP_EINVAL   -1   /* bad argument or shape */
+#define DNN_HIP_EDEVICE  -2   /* HIP runtime failure */
+#define DNN_HIP_ENOMEM   -3   /* device allocation failed */
+#define DNN_HIP_ERANGE   -4   /* KV cache / RoPE table / token id out of range */
+
+typedef struct dnn_hip_model dnn_hip_model;
+typedef struct dnn_hip_session dnn_hip_session;
+
+/* Message of the last failed call on this thread ("" if none). */
+const char *dnn_hip_last_error(void);
+
+/* Selects the device for this thread; idempotent. */
+int dnn_hip_init(int device);
+
+/* Mirrors a decoder LM's parameters into HBM (one upload; call again to
+ * refresh after the host weights change).  params holds 1 + 12*L + 2 pointers in
+ * module_parameters() order of the reference's decoder_lm:
+ *   embed.weight [V][D]
+ *   per block: qkv_proj.weight [D][3D], qkv_proj.bias [3D], out_proj.weight [D][D],
+ *              out_proj.bias [D], attn_norm.weight [D], ffn_norm.weight [D],
+ *              ffn.gate_proj.weight [D][F], .bias [F], ffn.up_proj.weight [D][F],
+ *              .bias [F], ffn.down_proj.weight [F][D], .bias [D]
+ *   norm.weight [D], lm_head.bias [V]
+ * eps: 2*L+1 RMSNorm epsilons (attn, ffn per block, then final) or NULL for 1e-5.
+ * Requires D == H*dk and dk == 64. */
+int dnn_hip_model_create(int vocab_size, int d_model, int n_layers, int n_heads,
+                         int d_k, int intermediate_size,
+                         const float *const *params, int n_params,
+                         const float *eps, dnn_hip_model **out);
+
+/* Re-uploads the parameters of an existing model (same shapes). */
+int dnn_hip_model_update(dnn_hip_model *m, const float *const *params, int n_params);
+
+/* Installs the RoPE tables cos/sin [rows][d_k/2] (NULL disables RoPE). */
+int dnn_hip_model_rope(dnn_hip_model *m, const float *cos_table,
+                       const float *sin_table, int rows);
+
+int dnn_hip_model_destroy(dnn_hip_model *m);
+
+/* A decode session: per-layer KV rings [B][H][max_seq][d_k] in HBM plus the
+ * activation arena.  Every row starts empty. */
+int dnn_hip_session_create(dnn_hip_model *m, int batch, int max_seq,
+                           dnn_hip_session **out);
+/* Empties every row (lengths back to 0). */
+int dnn_hip_session_reset(dnn_hip_session *s);
+/* Current cached length of each row -> lens[batch]. */
+int dnn_hip_session_lengths(dnn_hip_session *s, int *lens);
+int dnn_hip_session_destroy(dnn_hip_session *s);
+
+/* Runs n_steps decode steps on every row.  Step t of row b feeds
+ *   feed[t*batch + b]          while t < n_feed[b]   (n_feed NULL: n_feed_all)
+ *   the argmax of step t-1     afterwards (greedy)
+ * and appends one position to the row.  ids[t*batch + b] (nullable) receives the
+ * argmax of step t (first index of the maximum, as gpt.c:220-230); logits
+ * (nullable) receives the [n_steps][batch][V] rows.  With eos >= 0 the loop
+ * ends early once every row has produced eos in its greedy part; *steps_done
+ * (nullable) gets the number of steps run.  Requires n_feed >= 1 per row and
+ * length + n_steps <= max_seq (and <= RoPE rows). */
+int dnn_hip_decode(dnn_hip_session *s, const int *feed, int n_feed_all,
+                   const int *n_feed, int n_steps, int eos, int *ids,
+                   float *logits, int *steps_done);
+
+/* decoder_lm_generate(use_cache=1, temperature=0) for one sequence: out gets
+ * prompt + generated ids (P + max_new ints), *n_out its length (stops after eos
+ * when eos >= 0).  Uses a fresh session of max_seq = P + max_new. */
+int dnn_hip_generate(dnn_hip_model *m, const int *prompt, int n_prompt,
+                     int max_new, int eos, int *out, int *n_out);
+
+/* Device time of the last dnn_hip_decode call on this session, in ms, measured
+ * with HIP events around its kernel launches on the session's stream. */
+int dnn_hip_session_last_ms(dnn_hip_session *s, float *ms);
+
+/* Number of workgroups the persistent decode kernel runs with on this session
+ * (0 = choose the cooperative maximum) -- a tuning knob. */
+int dnn_hip_session_set_grid(dnn_hip_session *s, int n_workgroups);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

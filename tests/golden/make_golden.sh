@@ -1,0 +1,13 @@
+#!/bin/sh
+# Regenerates tests/golden/data/ from the real reference.  Dev container only:
+# needs /root/reference (the reference sources) and gcc.
+#   tests/golden/make_golden.sh [quick]
+set -e
+cd "$(dirname "$0")/../.."
+REF=${REF:-/root/reference}
+make -C oracle ref REF="$REF"
+mkdir -p oracle/_ref tests/golden/data
+gcc -std=gnu11 -O2 -include stdint.h -I"$REF/include" -I"$REF/src" -w \
+    tests/golden/gen_golden.c -o oracle/_ref/gen_golden \
+    -Loracle/_ref -ldnnref -Wl,-rpath,"$PWD/oracle/_ref" -lm
+OMP_NUM_THREADS=1 ./oracle/_ref/gen_golden "$@"

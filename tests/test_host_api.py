@@ -1,0 +1,35 @@
+"""Host side of the drop-in C API (include/dnn, libdnn_amd.so), no device:
+a caller written against the reference's API builds the same weights and prompt
+the reference built from the same seeds, and the DNNM state dict round-trips."""
+import json
+import os
+import subprocess
+
+import numpy as np
+import pytest
+
+
+def run(exe, *args):
+    out = subprocess.check_output([exe] + [str(a) for a in args], text=True, timeout=300)
+    return json.loads(out)
+
+
+@pytest.mark.parametrize("init,seed,pseed,key", [
+    ("synthetic", 1, 101, "c1"),
+    ("gpt2", 11, 111, "c1g"),
+])
+def test_c_api_builds_reference_weights_c1(generate_main, golden, init, seed, pseed, key):
+    r = run(generate_main, 128, 256, 4, 4, 683, 256, seed, init, pseed, 16, 0)
+    assert r["params"] == golden[key + "_params"]
+    assert r["tokens"] == golden[key + "_prompt"]
+
+
+def test_c_api_builds_reference_weights_c2(generate_main, golden):
+    r = run(generate_main, 8192, 768, 12, 12, 2048, 1088, 2, "synthetic", 102, 32, 0)
+    assert r["params"] == golden["c2_params"]
+    assert r["tokens"] == golden["c2_prompt"]
+
+
+def test_c_api_create_only_weights(generate_main, golden):
+    r = run(generate_main, 128, 256, 4, 4, 683, 256, 7, "create", 1, 4, 0)
+    assert r["params"] == golden["c1_create_params"]
