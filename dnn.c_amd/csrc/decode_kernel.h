@@ -56,7 +56,7 @@ struct DecodeArgs {
     int *ids;               // [n_steps][B]
     float *logits;          // [n_steps][B][V] or null
     int n_steps, eos;
-    unsigned long long *bar;
+    unsigned long long *bar;   // grid barrier: 10 counters, 256 bytes apart
     int *err;               // bit 0: a grid barrier wait hit its spin cap
     int *steps_done;
 };
@@ -66,6 +66,8 @@ struct DecodeArgs {
 inline size_t lds_bytes(int nb, int ldmax) {
     return sizeof(float) * (size_t)(3 * WPB * NBMAX + 3 * MAXB) + sizeof(float) * (size_t)nb * ldmax;
 }
+
+constexpr size_t BAR_WORDS = 10 * 32;
 
 const void *decode_kernel_for(int nb);
 

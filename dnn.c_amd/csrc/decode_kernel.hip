@@ -46,23 +46,45 @@ __device__ __forceinline__ f4 ld_stream(const float *p) {
     return __builtin_nontemporal_load(reinterpret_cast<const f4 *>(p));
 }
 
-// Grid-wide barrier over a monotonic counter (zeroed by the host before each
-// launch).  Stores made before it are visible to every workgroup after it:
-// release on arrival, relaxed polling (an acquire load would invalidate the
-// XCD's L2 on every poll), then one acquire fence.  The wait is bounded: after
-// SPIN_CAP polls the workgroup records the timeout in err[0] and proceeds, so
-// every wave reaches the end of the kernel whatever happens.
-constexpr unsigned SPIN_CAP = 1u << 26;
+// Grid-wide barrier.  Workgroups arrive on one of 8 sub-counters (blockIdx & 7:
+// consecutive workgroups are dealt round-robin over the 8 XCDs, so a
+// sub-counter collects one XCD's workgroups); the last arrival of a sub-group
+// arrives on the top counter, and the last top arrival publishes the barrier's
+// generation in a flag the others poll.  Two short chains of same-address
+// atomics instead of one long one; polls are relaxed (an acquire load would
+// invalidate the XCD's L2 on every poll) and one acquire fence follows.
+// Counters and flag are zeroed by the host before each launch.
+//
+// Every wait is bounded: after SPIN_CAP polls the workgroup sets err[0] and
+// goes on, and once err[0] is set every later barrier returns at once, so all
+// waves reach the end of the kernel whatever happens; the host discards the
+// results of such a launch.
+constexpr unsigned SPIN_CAP = 1u << 20;
+constexpr int BAR_STRIDE = 32;            // one 256-byte line per counter
 
-__device__ __forceinline__ void grid_sync(unsigned long long *ctr, unsigned long long &epoch, int *err) {
-    epoch += gridDim.x;
+__device__ __forceinline__ void grid_sync(unsigned long long *bar, unsigned long long &gen, int *err) {
+    gen++;
     __syncthreads();
-    if (threadIdx.x == 0) {
-        __hip_atomic_fetch_add(ctr, 1ull, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_AGENT);
-        unsigned it = 0;
-        while (__hip_atomic_load(ctr, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) < epoch) {
-            __builtin_amdgcn_s_sleep(1);
-            if (++it == SPIN_CAP) { atomicOr(err, 1); break; }
+    if (threadIdx.x == 0 && __hip_atomic_load(err, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == 0) {
+        const unsigned g = blockIdx.x & 7u;
+        const unsigned nsub = (gridDim.x - g + 7u) / 8u;
+        const unsigned ngrp = gridDim.x < 8u ? gridDim.x : 8u;
+        unsigned long long *sub = bar + g * BAR_STRIDE, *top = bar + 8 * BAR_STRIDE, *flag = bar + 9 * BAR_STRIDE;
+        bool published = false;
+        if (__hip_atomic_fetch_add(sub, 1ull, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_AGENT) == gen * nsub - 1) {
+            __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+            if (__hip_atomic_fetch_add(top, 1ull, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_AGENT) == gen * ngrp - 1) {
+                __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+                __hip_atomic_store(flag, gen, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_AGENT);
+                published = true;
+            }
+        }
+        if (!published) {
+            unsigned it = 0;
+            while (__hip_atomic_load(flag, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) < gen) {
+                __builtin_amdgcn_s_sleep(1);
+                if (++it == SPIN_CAP) { atomicOr(err, 1); break; }
+            }
         }
         __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
     }

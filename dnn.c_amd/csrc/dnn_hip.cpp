@@ -307,7 +307,7 @@ int dnn_hip_session_create(dnn_hip_model *m, int B, int max_seq, dnn_hip_session
     rc = rc ? rc : dalloc(&s->steps_done, 1);
     rc = rc ? rc : dalloc(&s->err, 1);
     rc = rc ? rc : dalloc(&s->att_cnt, (size_t)B * m->H);
-    rc = rc ? rc : dalloc(&s->bar, 1);
+    rc = rc ? rc : dalloc(&s->bar, BAR_WORDS);
     rc = rc ? rc : dalloc(&s->n_feed, (size_t)B);
     if (rc) { free_session_buffers(s); delete s; return rc; }
     hipError_t e = hipStreamCreateWithFlags(&s->stream, hipStreamNonBlocking);
@@ -362,6 +362,12 @@ int dnn_hip_session_set_grid(dnn_hip_session *s, int n) {
     return DNN_HIP_OK;
 }
 
+int dnn_hip_session_grid(dnn_hip_session *s, int *grid) {
+    if (!s || !grid) return fail(DNN_HIP_EINVAL, "NULL argument");
+    *grid = s->grid;
+    return DNN_HIP_OK;
+}
+
 int dnn_hip_session_last_ms(dnn_hip_session *s, float *ms) {
     if (!s || !ms) return fail(DNN_HIP_EINVAL, "NULL argument");
     *ms = s->last_ms;
@@ -374,6 +380,11 @@ int dnn_hip_decode(dnn_hip_session *s, const int *feed, int n_feed_all, const in
     dnn_hip_model *m = s->m;
     const int B = s->B;
     if (n_steps <= 0) return fail(DNN_HIP_EINVAL, "n_steps %d", n_steps);
+    // More than NBMAX rows means several batch groups inside one launch.  That
+    // path faulted the GPU once (B=32) and the cause has not been shown, so it
+    // stays switched off until it is.
+    if (B > NBMAX)
+        return fail(DNN_HIP_EINVAL, "batch %d > %d rows per decode launch is disabled", B, NBMAX);
     std::vector<int> nf(B);
     int nf_max = 0;
     for (int b = 0; b < B; b++) {
@@ -399,20 +410,24 @@ int dnn_hip_decode(dnn_hip_session *s, const int *feed, int n_feed_all, const in
     if (rc) return rc;
     HIP_TRY(hipMemcpyAsync(s->feed, feed, sizeof(int) * (size_t)nf_max * B, hipMemcpyHostToDevice, s->stream));
     HIP_TRY(hipMemcpyAsync(s->n_feed, nf.data(), sizeof(int) * B, hipMemcpyHostToDevice, s->stream));
-    HIP_TRY(hipMemsetAsync(s->bar, 0, sizeof(unsigned long long), s->stream));
+    HIP_TRY(hipMemsetAsync(s->bar, 0, sizeof(unsigned long long) * BAR_WORDS, s->stream));
     HIP_TRY(hipMemsetAsync(s->err, 0, sizeof(int), s->stream));
 
     const int nb = pick_nb(B);
     const void *kern = decode_kernel_for(nb);
     const size_t shmem = lds_bytes(nb, std::max(m->ldD, m->ldF));
     HIP_TRY(hipFuncSetAttribute(kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)shmem));
+    // One workgroup per CU by default: every workgroup must be resident at once
+    // for the grid barriers, and fewer arrivals make each barrier cheaper.  The
+    // launch is a plain one (a cooperative launch would tie the global wave-sync
+    // resource to this process); the barrier's bounded waits keep a launch that
+    // could not be co-scheduled from hanging.
     int per_cu = 0, n_cu = 0;
     HIP_TRY(hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kern, BLOCK, shmem));
     HIP_TRY(hipDeviceGetAttribute(&n_cu, hipDeviceAttributeMultiprocessorCount, m->device));
-    int grid = per_cu * n_cu;
-    if (s->grid_req > 0) grid = std::min(grid, s->grid_req);
+    if (per_cu <= 0) return fail(DNN_HIP_EDEVICE, "decode kernel does not fit on a CU (shmem %zu)", shmem);
+    int grid = s->grid_req > 0 ? std::min(s->grid_req, per_cu * n_cu) : n_cu;
     grid = std::min(grid, s->grid_cap);
-    if (grid <= 0) return fail(DNN_HIP_EDEVICE, "decode kernel does not fit on a CU (shmem %zu)", shmem);
     s->grid = grid;
 
     DecodeArgs a{};
@@ -427,7 +442,7 @@ int dnn_hip_decode(dnn_hip_session *s, const int *feed, int n_feed_all, const in
     a.n_steps = n_steps; a.eos = eos; a.bar = s->bar; a.err = s->err; a.steps_done = s->steps_done;
     void *kargs[] = {&a};
     HIP_TRY(hipEventRecord(s->ev0, s->stream));
-    HIP_TRY(hipLaunchCooperativeKernel(kern, dim3(grid), dim3(BLOCK), kargs, (unsigned)shmem, s->stream));
+    HIP_TRY(hipLaunchKernel(kern, dim3(grid), dim3(BLOCK), kargs, (unsigned)shmem, s->stream));
     HIP_TRY(hipEventRecord(s->ev1, s->stream));
     HIP_TRY(hipEventSynchronize(s->ev1));
     HIP_TRY(hipEventElapsedTime(&s->last_ms, s->ev0, s->ev1));

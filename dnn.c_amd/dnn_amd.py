@@ -23,6 +23,7 @@ HIP_SYMBOLS = [
     "dnn_hip_model_rope", "dnn_hip_model_destroy", "dnn_hip_session_create",
     "dnn_hip_session_reset", "dnn_hip_session_lengths", "dnn_hip_session_destroy",
     "dnn_hip_decode", "dnn_hip_generate", "dnn_hip_session_last_ms", "dnn_hip_session_set_grid",
+    "dnn_hip_session_grid",
 ]
 
 
@@ -54,6 +55,7 @@ def hip():
         L.dnn_hip_generate.argtypes = [C.c_void_p, i32p, C.c_int, C.c_int, C.c_int, i32p, i32p]
         L.dnn_hip_session_last_ms.argtypes = [C.c_void_p, f32p]
         L.dnn_hip_session_set_grid.argtypes = [C.c_void_p, C.c_int]
+        L.dnn_hip_session_grid.argtypes = [C.c_void_p, i32p]
         _hip = L
     return _hip
 
@@ -113,6 +115,11 @@ class HipSession:
         h = C.c_void_p()
         check(hip().dnn_hip_session_create(model.ptr, batch, max_seq, C.byref(h)))
         self.ptr = h
+
+    def grid(self):
+        g = C.c_int()
+        check(hip().dnn_hip_session_grid(self.ptr, C.byref(g)))
+        return g.value
 
     def set_grid(self, n):
         check(hip().dnn_hip_session_set_grid(self.ptr, n))

@@ -122,3 +122,5 @@ void decoder_lm_device_release(decoder_lm *lm) {
     m->lm = NULL;
     m->dm = NULL;
 }
+
+struct dnn_hip_model *decoder_lm_device_model(decoder_lm *lm) { return dnn_amd_device_model(lm); }

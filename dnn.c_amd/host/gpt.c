@@ -89,6 +89,19 @@ void decoder_lm_init_weights(decoder_lm *lm) {
     init_walk(&lm->base, std, residual_std);
 }
 
+void decoder_lm_init_normal(decoder_lm *lm, float std) {
+    int n;
+    tensor **ps = module_parameters(&lm->base, &n);
+    for (int i = 0; i < n; i++) {
+        int gamma = ps[i] == lm->norm->weight;
+        for (int l = 0; l < lm->n_layers; l++)
+            gamma |= ps[i] == lm->blocks[l]->attn_norm->weight || ps[i] == lm->blocks[l]->ffn_norm->weight;
+        if (gamma) continue;
+        float *d = tensor_data_ptr(ps[i]);
+        for (int j = 0, ne = tensor_numel(ps[i]); j < ne; j++) d[j] = dnn_rng_normal(dnn_get_rng()) * std;
+    }
+}
+
 void decoder_lm_enable_rope(struct mem_pool *params_pool, decoder_lm *lm, int max_seq_len, float base) {
     assert(lm && max_seq_len > 0);
     const int d_k = lm->blocks[0]->d_k;

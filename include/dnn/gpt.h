@@ -42,5 +42,14 @@ int *decoder_lm_generate(struct mem_pool *scratch_pool, struct mem_pool *data_po
  * weights in place); decoder_lm_device_release frees the mirror. */
 void decoder_lm_device_sync(decoder_lm *lm);
 void decoder_lm_device_release(decoder_lm *lm);
+/* The mirror itself, for callers that drive sessions through include/dnn_hip.h
+ * (batched decode, timing).  Owned by the library. */
+struct dnn_hip_model *decoder_lm_device_model(decoder_lm *lm);
+
+/* Synthetic initialisation used by the parity and bench configurations (no
+ * counterpart in the reference): every parameter except the RMSNorm gammas is
+ * redrawn as dnn_rng_normal() * std from the default stream, in
+ * module_parameters() order. */
+void decoder_lm_init_normal(decoder_lm *lm, float std);
 
 #endif

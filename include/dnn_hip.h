@@ -98,7 +98,8 @@ int dnn_hip_session_destroy(dnn_hip_session *s);
  * (nullable) receives the [n_steps][batch][V] rows.  With eos >= 0 the loop
  * ends early once every row has produced eos in its greedy part; *steps_done
  * (nullable) gets the number of steps run.  Requires n_feed >= 1 per row and
- * length + n_steps <= max_seq (and <= RoPE rows). */
+ * length + n_steps <= max_seq (and <= RoPE rows).  At most 8 rows per call for
+ * now (larger batches return DNN_HIP_EINVAL). */
 int dnn_hip_decode(dnn_hip_session *s, const int *feed, int n_feed_all,
                    const int *n_feed, int n_steps, int eos, int *ids,
                    float *logits, int *steps_done);
@@ -116,6 +117,8 @@ int dnn_hip_session_last_ms(dnn_hip_session *s, float *ms);
 /* Number of workgroups the persistent decode kernel runs with on this session
  * (0 = choose the cooperative maximum) -- a tuning knob. */
 int dnn_hip_session_set_grid(dnn_hip_session *s, int n_workgroups);
+/* Workgroups the last dnn_hip_decode launch on this session used. */
+int dnn_hip_session_grid(dnn_hip_session *s, int *n_workgroups);
 
 #ifdef __cplusplus
 }

@@ -1,0 +1,176 @@
+"""GPU parity of the decode path against the oracle (itself bit-pinned to the
+reference by test_oracle_golden.py) and the reference's fixtures.
+
+Bars:
+  * greedy token sequences identical to the reference's;
+  * per-step logits within max-abs 1e-3 and relative 1e-4, the relative error
+    being max|dlogit| / max|logit| over the step's vocabulary row.
+"""
+import json
+import subprocess
+
+import numpy as np
+import pytest
+
+import dnn_amd as A
+import oracle_lib as O
+from golden_util import binf
+
+pytestmark = pytest.mark.gpu
+
+ABS_TOL = 1e-3
+REL_TOL = 1e-4
+
+
+def assert_logits_close(got, want, what):
+    got = np.asarray(got, dtype=np.float64)
+    want = np.asarray(want, dtype=np.float64)
+    err = np.abs(got - want).max(axis=-1)
+    scale = np.abs(want).max(axis=-1)
+    assert err.max() <= ABS_TOL, "%s: max |dlogit| %.3g" % (what, err.max())
+    assert (err / scale).max() <= REL_TOL, "%s: max relative %.3g" % (what, (err / scale).max())
+
+
+def hip_model(m):
+    return A.HipModel(m.V, m.D, m.L, m.H, m.F, m.params(), rope=m.rope_tables())
+
+
+@pytest.fixture(scope="module")
+def c1():
+    return O.Model(128, 256, 4, 4, 683, 256, seed=1)
+
+
+@pytest.fixture(scope="module")
+def c1g():
+    return O.Model(128, 256, 4, 4, 683, 256, seed=11, init="gpt2")
+
+
+@pytest.fixture(scope="module")
+def c2():
+    m = O.Model(8192, 768, 12, 12, 2048, 1088, seed=2)
+    return m, hip_model(m)
+
+
+@pytest.mark.parametrize("tag", ["c1", "c1g"])
+def test_c1_greedy_tokens_and_logits(golden, c1, c1g, tag):
+    m = c1 if tag == "c1" else c1g
+    hm = hip_model(m)
+    prompt = np.array(golden[tag + "_prompt"], dtype=np.int32)
+    assert list(hm.generate(prompt, 240)) == golden[tag + "_tokens"]
+    # teacher-forced on the reference's own ids: every step's logits
+    s = A.HipSession(hm, 1, 256)
+    toks = golden[tag + "_tokens"]
+    _, lg = s.decode(np.array(toks[:-1]), len(toks) - 1, want_logits=True)
+    assert_logits_close(lg[15:, 0], binf(tag + "_logits.f32", 128), tag)
+
+
+def test_c2_tokens_match_reference(golden, c2):
+    """The headline config: 32-token prompt, 512 greedy tokens, all identical."""
+    _, hm = c2
+    out = hm.generate(np.array(golden["c2_prompt"], dtype=np.int32), 512)
+    assert list(out) == golden["c2_tokens"]
+
+
+def test_c2_logits_first_steps(golden, c2):
+    _, hm = c2
+    s = A.HipSession(hm, 1, 64)
+    toks = golden["c2_tokens"][:36]
+    _, lg = s.decode(np.array(toks[:-1]), 35, want_logits=True)
+    assert_logits_close(lg[31:, 0], binf("c2_logits4.f32", 8192), "c2 first 4 steps")
+
+
+def test_c2_logits_late_steps_vs_oracle(golden, c2):
+    """Teacher-forced positions 256..287 (KV history of up to 288 keys: five
+    64-key attention chunks combined across workgroups)."""
+    m, hm = c2
+    toks = np.array(golden["c2_tokens"], dtype=np.int32)
+    st = O.State(m, 288)
+    h = st.forward(O.embed(m, toks[:288]))    # one cached pass over 288 rows
+    want = O.head(m, h[-32:])
+    s = A.HipSession(hm, 1, 288)
+    _, lg = s.decode(toks[:288], 288, want_logits=True)
+    assert_logits_close(lg[-32:, 0], want, "c2 positions 256-287")
+
+
+def test_c2_gpt2_init_tokens(golden):
+    m = O.Model(8192, 768, 12, 12, 2048, 1088, seed=12, init="gpt2")
+    hm = hip_model(m)
+    want = golden["c2g_tokens"]
+    out = hm.generate(np.array(golden["c2g_prompt"], dtype=np.int32), len(want) - 32)
+    assert list(out) == want
+
+
+@pytest.mark.parametrize("B", [2, 5, 8])
+def test_batch_rows_match_independent_runs(c1g, B):
+    """Each row of a batched decode equals its own B=1 run (rows differ in
+    prompt length, so they switch from prompt to greedy at different steps)."""
+    hm = hip_model(c1g)
+    rng = np.random.default_rng(B)
+    lens = rng.integers(1, 9, size=B).astype(np.int32)
+    feed = rng.integers(0, 128, size=(8, B)).astype(np.int32)
+    steps = 40
+    s = A.HipSession(hm, B, 64)
+    ids, lg = s.decode(feed, steps, n_feed=lens, want_logits=True)
+    for b in range(B):
+        want, wlg = c1g.generate(feed[: lens[b], b], steps - lens[b] + 1, eos=-1, want_logits=True)
+        got = list(feed[: lens[b], b]) + list(ids[lens[b] - 1:, b])
+        assert got == list(want), "row %d" % b
+        assert_logits_close(lg[lens[b] - 1:, b], wlg, "row %d" % b)
+    assert list(s.lengths()) == [steps] * B
+
+
+def test_eos_stops_generation():
+    """A bias pushing id 258 to the top makes the first generated token EOS: the
+    run stops there (gpt.c:339), on the device as in the oracle."""
+    m = O.Model(300, 128, 2, 2, 256, 64, seed=3, init="gpt2")
+    p = m.params()
+    p[-1][258] = 50.0                      # lm_head.bias
+    hm = A.HipModel(300, 128, 2, 2, 256, p, rope=m.rope_tables())
+    prompt = O.prompt_ids(9, 300, 5)
+    out = hm.generate(prompt, 20)
+    assert list(out) == list(prompt) + [258]
+
+
+def test_session_bounds_are_errors(c1g):
+    hm = hip_model(c1g)
+    s = A.HipSession(hm, 1, 8)
+    with pytest.raises(A.HipError, match="max_seq"):
+        s.decode(np.array([1]), 9)
+    with pytest.raises(A.HipError, match="outside"):
+        s.decode(np.array([128]), 1)
+    ids, _ = s.decode(np.array([1]), 8)
+    assert len(ids) == 8
+    with pytest.raises(A.HipError, match="max_seq"):
+        s.decode(ids[-1:], 1)
+    s.reset()
+    assert list(s.lengths()) == [0]
+
+
+def test_large_batch_is_refused(c1g):
+    hm = hip_model(c1g)
+    s = A.HipSession(hm, 9, 16)
+    with pytest.raises(A.HipError, match="disabled"):
+        s.decode(np.zeros((1, 9), dtype=np.int32), 1)
+
+
+@pytest.mark.parametrize("init,seed,pseed,key", [("synthetic", 1, 101, "c1"), ("gpt2", 11, 111, "c1g")])
+def test_c_api_generate_matches_reference(generate_main, golden, init, seed, pseed, key):
+    """A C caller of decoder_lm_generate (the reference's API) gets the
+    reference's ids, weights built by the same API calls."""
+    out = subprocess.check_output([generate_main, "128", "256", "4", "4", "683", "256", str(seed), init,
+                                   str(pseed), "16", "240"], text=True, timeout=300)
+    r = json.loads(out)
+    assert r["params"] == golden[key + "_params"]
+    assert r["tokens"] == golden[key + "_tokens"]
+
+
+def test_c_api_nocache_and_sampling(generate_main, golden):
+    nc = json.loads(subprocess.check_output([generate_main, "128", "256", "4", "4", "683", "256", "1",
+                                             "synthetic", "101", "16", "24", "0", "0"], text=True, timeout=300))
+    assert nc["tokens"] == golden["c1_nocache_tokens"]
+    a = subprocess.check_output([generate_main, "128", "256", "4", "4", "683", "256", "11", "gpt2",
+                                 "111", "16", "32", "0.8"], text=True, timeout=300)
+    b = subprocess.check_output([generate_main, "128", "256", "4", "4", "683", "256", "11", "gpt2",
+                                 "111", "16", "32", "0.8"], text=True, timeout=300)
+    ra, rb = json.loads(a), json.loads(b)
+    assert ra["tokens"] == rb["tokens"] and len(ra["tokens"]) == 48
