@@ -2,73 +2,98 @@
 // the C-ABI layer (dnn_hip.cpp).  Internal: not part of the public headers.
 #pragma once
 #include <hip/hip_runtime.h>
+#include <stdint.h>
 
 namespace dnnhip {
 
 constexpr int WAVE = 64;          // CDNA wavefront
-constexpr int BLOCK = 256;        // threads per workgroup
-constexpr int WPB = BLOCK / WAVE; // wavefronts per workgroup
-constexpr int NBMAX = 8;          // batch rows per GEMV pass
-constexpr int CH = 64;            // cached keys per attention work unit
+constexpr int BLOCK = 512;        // threads per workgroup (8 wavefronts, 2 per SIMD)
+constexpr int WPB = BLOCK / WAVE;
+constexpr int CH = 32;            // cached keys per attention work unit (two half-waves per key)
 constexpr int DK = 64;            // head dimension the kernels are built for
-constexpr int MAXB = 256;         // batch rows per session
-constexpr int LDALIGN = 256;      // out-major weight rows padded to this many floats
+constexpr int MAXB = 8;           // batch rows per decode launch
+constexpr int LDALIGN = 256;      // weight rows / activation rows padded to this many floats
 
-// One transformer block in HBM.  All weight matrices are out-major: row n holds
-// the K inputs of output n, zero-padded to ld (= K rounded up to LDALIGN).
-struct LayerW {
-    const float *wqkv;   // [3D][ldD]  rows 0..D-1 = Q, D..2D-1 = K, 2D..3D-1 = V
-    const float *bqkv;   // [3D]
-    const float *wo;     // [D][ldD]
-    const float *bo;     // [D]
-    const float *g_attn; // [ldD]
-    const float *g_ffn;  // [ldD]
-    const float *wgu;    // [F][2][ldD]  gate row f, then up row f
-    const float *bg;     // [F]
-    const float *bu;     // [F]
-    const float *wd;     // [D][ldF]
-    const float *bd;     // [D]
+// One transformer block inside the weight arena, as float offsets from its
+// base.  Weight matrices are out-major: row n holds the K inputs of output n,
+// zero-padded to ld (= K rounded up to LDALIGN).
+struct LayerOff {
+    uint32_t wqkv;   // [3D][ldD]  rows 0..D-1 = Q, D..2D-1 = K, 2D..3D-1 = V
+    uint32_t bqkv;   // [3D]
+    uint32_t wo;     // [D][ldD]
+    uint32_t bo;     // [D]
+    uint32_t g_attn; // [ldD]
+    uint32_t g_ffn;  // [ldD]
+    uint32_t wgu;    // [F][2][ldD]  gate row f, then up row f
+    uint32_t bg;     // [F]
+    uint32_t bu;     // [F]
+    uint32_t wd;     // [D][ldF]
+    uint32_t bd;     // [D]
     float eps_attn, eps_ffn;
+};
+
+// Exchange arena: every value one wavefront hands to another travels as an
+// 8-byte (value bits, tag) pair written with one coherent (sc1) store; the tag
+// is the global step id, so a reader knows a value is this step's by its tag
+// and no barrier is needed.  Per layer and batch row:
+//   X1 [ldD]  residual stream after attention    X2 [ldD]  after the FFN
+//   Q, KN, VN [D]  this step's query and new key/value rows (K after RoPE)
+//   ATT [D]   merged attention heads            ACT [ldF] SwiGLU output
+//   PART [H][nch_cap][DK+2]  split-S attention partials (o[DK], max, sum)
+// then the lm_head argmax partials AMAX [2][B][grid][2] (value, index), double
+// buffered by step parity: a workgroup overwrites its step-t slot at step t+2
+// only after reading every workgroup's step-(t+1) partial, each written after
+// its writer finished reading the step-t partials.
+struct Exch {
+    int ldD, ldF, D, H, nch_cap, B, grid;
+    __host__ __device__ size_t per_row() const { return (size_t)2 * ldD + 4 * (size_t)D + ldF + (size_t)H * nch_cap * (DK + 2); }
+    __host__ __device__ size_t per_layer() const { return per_row() * B; }
+    __host__ __device__ size_t base(int l, int b) const { return per_layer() * l + per_row() * b; }
+    __host__ __device__ size_t x1(int l, int b) const { return base(l, b); }
+    __host__ __device__ size_t x2(int l, int b) const { return base(l, b) + ldD; }
+    __host__ __device__ size_t q(int l, int b) const { return base(l, b) + 2 * (size_t)ldD; }
+    __host__ __device__ size_t kn(int l, int b) const { return q(l, b) + D; }
+    __host__ __device__ size_t vn(int l, int b) const { return q(l, b) + 2 * (size_t)D; }
+    __host__ __device__ size_t att(int l, int b) const { return q(l, b) + 3 * (size_t)D; }
+    __host__ __device__ size_t act(int l, int b) const { return q(l, b) + 4 * (size_t)D; }
+    __host__ __device__ size_t part(int l, int b, int h, int c) const {
+        return act(l, b) + ldF + ((size_t)h * nch_cap + c) * (DK + 2);
+    }
+    __host__ __device__ size_t amax(int L, int par, int b, int g) const {
+        return per_layer() * L + (((size_t)par * B + b) * grid + g) * 2;
+    }
+    __host__ __device__ size_t total(int L) const { return per_layer() * L + (size_t)2 * B * grid * 2; }
 };
 
 struct DecodeArgs {
     int V, D, L, H, F, ldD, ldF;
-    const LayerW *layers;   // [L], device
-    const float *embed;     // [V][ldD] (also the tied lm_head)
-    const float *lm_bias;   // [V]
-    const float *g_final;   // [ldD]
+    const float *wts;       // weight arena: embedding [V][ldD] (also the tied
+    uint32_t wts_bytes;     // lm_head), lm_head bias, final gamma, the blocks
+    uint32_t embed, lm_bias, g_final;   // float offsets in the arena
+    const LayerOff *layers; // [L], device
     float eps_final;
-    const float *rope_cos;  // [rope_rows][DK/2] or null
-    const float *rope_sin;
-    int B, max_seq, nch_cap;
-    float *x;               // [B][ldD] residual stream
-    float *q;               // [B][H][DK]
-    float *att;             // [B][ldD] merged heads
-    float *act;             // [B][ldF] SwiGLU output
-    float *kc, *vc;         // [L][B][H][max_seq][DK]
+    const float *rope;      // [2][rope_rows][DK/2]: cos rows, then sin rows; or null
+    int rope_rows;
+    int B, max_seq;
+    float *kc;              // K^T cache [L][B][H][DK][max_seq]
+    float *vc;              // V cache   [L][B][H][max_seq][DK]
+    uint2 *xa;              // exchange arena (Exch layout), pairs
+    Exch ex;
     int *pos;               // [B] cached length per row (in/out)
-    float *part;            // [B][H][nch_cap][DK+2] attention partials (m, l, o[DK])
-    unsigned *att_cnt;      // [B][H] arrival counters (left at 0)
-    float *amax_v;          // [B][grid] per-workgroup argmax partials
-    int *amax_i;
-    const int *feed;        // [n_feed_max][B]
+    const int *feed;        // [max n_feed][B]
     const int *n_feed;      // [B]
     int *ids;               // [n_steps][B]
     float *logits;          // [n_steps][B][V] or null
     int n_steps, eos;
-    unsigned long long *bar;   // grid barrier: 10 counters, 256 bytes apart
-    int *err;               // bit 0: a grid barrier wait hit its spin cap
+    unsigned step0;         // tag of this launch's first step (>= 1, increasing)
+    int *err;               // bit 0: a dependency wait hit its spin cap
     int *steps_done;
 };
 
-// Dynamic LDS of decode_persistent<nb>: the fixed per-workgroup arrays plus nb
-// staged activation rows of ldmax floats.
-inline size_t lds_bytes(int nb, int ldmax) {
-    return sizeof(float) * (size_t)(3 * WPB * NBMAX + 3 * MAXB) + sizeof(float) * (size_t)nb * ldmax;
-}
+// Dynamic LDS of the decode kernel: per-row token / position / done flags and
+// the per-wavefront argmax scratch.
+inline size_t lds_bytes() { return sizeof(int) * (3 * MAXB + 2 * WPB * MAXB); }
 
-constexpr size_t BAR_WORDS = 10 * 32;
-
-const void *decode_kernel_for(int nb);
+const void *decode_kernel_for(int nb, int dc);
 
 }  // namespace dnnhip

@@ -43,12 +43,10 @@ struct dnn_hip_model {
     int device;
     char *arena = nullptr;
     size_t arena_bytes = 0;
-    std::vector<LayerW> layers;      // device pointers
-    LayerW *d_layers = nullptr;
-    float *embed = nullptr, *lm_bias = nullptr, *g_final = nullptr;
+    LayerOff *d_layers = nullptr;    // [L] float offsets of each block's tensors
     float eps_final = 1e-5f;
     std::vector<float> eps;          // 2L+1
-    float *rope_cos = nullptr, *rope_sin = nullptr;
+    float *rope = nullptr;           // [2][rope_rows][dk/2]: cos, then sin
     int rope_rows = 0;
     // byte offsets of every device tensor inside the arena, for the uploads
     struct Off { size_t embed, lm_bias, g_final; std::vector<size_t> l; } off;
@@ -59,16 +57,16 @@ struct dnn_hip_session {
     int B, max_seq, nch_cap;
     hipStream_t stream = nullptr;
     hipEvent_t ev0 = nullptr, ev1 = nullptr;
-    float *x = nullptr, *q = nullptr, *att = nullptr, *act = nullptr, *kc = nullptr, *vc = nullptr;
-    float *part = nullptr, *amax_v = nullptr;
-    int *amax_i = nullptr, *pos = nullptr, *steps_done = nullptr, *err = nullptr;
-    unsigned *att_cnt = nullptr;
-    unsigned long long *bar = nullptr;
+    float *kc = nullptr, *vc = nullptr;       // K^T [L][B][H][DK][max_seq], V [L][B][H][max_seq][DK]
+    uint2 *xa = nullptr;                      // exchange arena (tagged pairs)
+    Exch ex{};
+    int *pos = nullptr, *steps_done = nullptr, *err = nullptr;
     int *feed = nullptr, *n_feed = nullptr, *ids = nullptr;
     size_t feed_cap = 0, ids_cap = 0;
     float *logits = nullptr;
     size_t logits_cap = 0;
     int grid_req = 0, grid = 0, grid_cap = 0;
+    unsigned next_tag = 1;                    // tags only grow: stale values never match
     float last_ms = 0.f;
     std::vector<int> h_pos;
 };
@@ -150,8 +148,7 @@ int upload(dnn_hip_model *m, const float *const *params, int n_params) {
 }
 
 void free_session_buffers(dnn_hip_session *s) {
-    void *bufs[] = {s->x, s->q, s->att, s->act, s->kc, s->vc, s->part, s->amax_v, s->amax_i, s->pos,
-                    s->steps_done, s->err, s->att_cnt, s->bar, s->feed, s->n_feed, s->ids, s->logits};
+    void *bufs[] = {s->kc, s->vc, s->xa, s->pos, s->steps_done, s->err, s->feed, s->n_feed, s->ids, s->logits};
     for (void *p : bufs)
         if (p) (void)hipFree(p);
 }
@@ -174,7 +171,7 @@ int grow(T **p, size_t *cap, size_t count) {
     return rc;
 }
 
-int pick_nb(int B) { return B >= 8 ? 8 : B >= 4 ? 4 : B >= 2 ? 2 : 1; }
+int pick_nb(int B) { return B > 4 ? 8 : B > 2 ? 4 : B > 1 ? 2 : 1; }
 
 }  // namespace
 
@@ -199,6 +196,7 @@ int dnn_hip_model_create(int V, int D, int L, int H, int dk, int F, const float 
     if (D != H * dk) return fail(DNN_HIP_EINVAL, "d_model %d != n_heads %d * d_k %d", D, H, dk);
     if (dk != DK) return fail(DNN_HIP_EINVAL, "the decode kernels are built for d_k=%d (got %d)", DK, dk);
     if (D % 2 || V % 2) return fail(DNN_HIP_EINVAL, "d_model and vocab_size must be even");
+    if (D > 3 * LDALIGN) return fail(DNN_HIP_EINVAL, "d_model %d: the decode kernels cover d_model <= %d", D, 3 * LDALIGN);
     int dev = 0;
     HIP_TRY(hipGetDevice(&dev));
     auto *m = new dnn_hip_model();
@@ -210,28 +208,31 @@ int dnn_hip_model_create(int V, int D, int L, int H, int dk, int F, const float 
     if (eps) for (int i = 0; i < 2 * L + 1; i++) m->eps[i] = eps[i];
     m->eps_final = m->eps[2 * L];
     plan_layout(m);
+    // every access goes through 32-bit buffer offsets
+    if (m->arena_bytes >= 0x7fffffffu) {
+        const size_t bytes = m->arena_bytes;
+        delete m;
+        return fail(DNN_HIP_EINVAL, "weights need %zu bytes; one decode arena holds < 2 GiB", bytes);
+    }
     hipError_t e = hipMalloc(reinterpret_cast<void **>(&m->arena), m->arena_bytes);
     if (e != hipSuccess) { delete m; return fail(DNN_HIP_ENOMEM, "hipMalloc(%zu) for weights: %s", m->arena_bytes, hipGetErrorString(e)); }
     int rc = upload(m, params, n_params);
     if (rc != DNN_HIP_OK) { (void)hipFree(m->arena); delete m; return rc; }
-    auto dp = [&](size_t off) { return reinterpret_cast<float *>(m->arena + off); };
-    m->embed = dp(m->off.embed);
-    m->lm_bias = dp(m->off.lm_bias);
-    m->g_final = dp(m->off.g_final);
-    m->layers.resize(L);
+    auto fo = [](size_t byte_off) { return (uint32_t)(byte_off / sizeof(float)); };
+    std::vector<LayerOff> lo(L);
     for (int l = 0; l < L; l++) {
         const size_t *o = &m->off.l[(size_t)l * NPL];
-        LayerW &w = m->layers[l];
-        w.wqkv = dp(o[P_WQKV]); w.bqkv = dp(o[P_BQKV]);
-        w.wo = dp(o[P_WO]); w.bo = dp(o[P_BO]);
-        w.g_attn = dp(o[P_GA]); w.g_ffn = dp(o[P_GF]);
-        w.wgu = dp(o[P_WG]); w.bg = dp(o[P_BG]); w.bu = dp(o[P_BU]);
-        w.wd = dp(o[P_WD]); w.bd = dp(o[P_BD]);
+        LayerOff &w = lo[l];
+        w.wqkv = fo(o[P_WQKV]); w.bqkv = fo(o[P_BQKV]);
+        w.wo = fo(o[P_WO]); w.bo = fo(o[P_BO]);
+        w.g_attn = fo(o[P_GA]); w.g_ffn = fo(o[P_GF]);
+        w.wgu = fo(o[P_WG]); w.bg = fo(o[P_BG]); w.bu = fo(o[P_BU]);
+        w.wd = fo(o[P_WD]); w.bd = fo(o[P_BD]);
         w.eps_attn = m->eps[2 * l];
         w.eps_ffn = m->eps[2 * l + 1];
     }
-    e = hipMalloc(reinterpret_cast<void **>(&m->d_layers), sizeof(LayerW) * L);
-    if (e == hipSuccess) e = hipMemcpy(m->d_layers, m->layers.data(), sizeof(LayerW) * L, hipMemcpyHostToDevice);
+    e = hipMalloc(reinterpret_cast<void **>(&m->d_layers), sizeof(LayerOff) * L);
+    if (e == hipSuccess) e = hipMemcpy(m->d_layers, lo.data(), sizeof(LayerOff) * L, hipMemcpyHostToDevice);
     if (e != hipSuccess) {
         (void)hipFree(m->arena);
         if (m->d_layers) (void)hipFree(m->d_layers);
@@ -250,18 +251,15 @@ int dnn_hip_model_update(dnn_hip_model *m, const float *const *params, int n_par
 int dnn_hip_model_rope(dnn_hip_model *m, const float *cos_table, const float *sin_table, int rows) {
     if (!m) return fail(DNN_HIP_EINVAL, "model is NULL");
     HIP_TRY(hipSetDevice(m->device));
-    if (m->rope_cos) { (void)hipFree(m->rope_cos); m->rope_cos = nullptr; }
-    if (m->rope_sin) { (void)hipFree(m->rope_sin); m->rope_sin = nullptr; }
+    if (m->rope) { (void)hipFree(m->rope); m->rope = nullptr; }
     m->rope_rows = 0;
     if (!cos_table || !sin_table) return DNN_HIP_OK;
     if (rows <= 0) return fail(DNN_HIP_EINVAL, "rope rows %d", rows);
     const size_t n = (size_t)rows * (m->dk / 2);
-    int rc = dalloc(&m->rope_cos, n);
+    int rc = dalloc(&m->rope, 2 * n);
     if (rc) return rc;
-    rc = dalloc(&m->rope_sin, n);
-    if (rc) return rc;
-    HIP_TRY(hipMemcpy(m->rope_cos, cos_table, n * sizeof(float), hipMemcpyHostToDevice));
-    HIP_TRY(hipMemcpy(m->rope_sin, sin_table, n * sizeof(float), hipMemcpyHostToDevice));
+    HIP_TRY(hipMemcpy(m->rope, cos_table, n * sizeof(float), hipMemcpyHostToDevice));
+    HIP_TRY(hipMemcpy(m->rope + n, sin_table, n * sizeof(float), hipMemcpyHostToDevice));
     m->rope_rows = rows;
     return DNN_HIP_OK;
 }
@@ -271,8 +269,7 @@ int dnn_hip_model_destroy(dnn_hip_model *m) {
     (void)hipSetDevice(m->device);
     if (m->arena) (void)hipFree(m->arena);
     if (m->d_layers) (void)hipFree(m->d_layers);
-    if (m->rope_cos) (void)hipFree(m->rope_cos);
-    if (m->rope_sin) (void)hipFree(m->rope_sin);
+    if (m->rope) (void)hipFree(m->rope);
     delete m;
     return DNN_HIP_OK;
 }
@@ -289,37 +286,34 @@ int dnn_hip_session_create(dnn_hip_model *m, int B, int max_seq, dnn_hip_session
     s->max_seq = max_seq;
     s->nch_cap = (max_seq + CH - 1) / CH;
     s->h_pos.assign(B, 0);
+    int n_cu = 0;
+    if (hipDeviceGetAttribute(&n_cu, hipDeviceAttributeMultiprocessorCount, m->device) != hipSuccess || n_cu <= 0) n_cu = 256;
+    s->grid_cap = n_cu;
+    s->ex = Exch{m->ldD, m->ldF, m->D, m->H, s->nch_cap, B, s->grid_cap};
     const size_t kv = (size_t)m->L * B * m->H * max_seq * DK;
+    const size_t xa_pairs = s->ex.total(m->L);
+    if (kv * sizeof(float) >= 0x7fffffffu || xa_pairs * 8 >= 0x7fffffffu) {
+        delete s;
+        return fail(DNN_HIP_EINVAL, "KV cache of %zu bytes per tensor / exchange of %zu bytes: each must stay < 2 GiB",
+                    kv * sizeof(float), xa_pairs * 8);
+    }
     int rc = 0;
-    int dev_cu = 0;
-    if (hipDeviceGetAttribute(&dev_cu, hipDeviceAttributeMultiprocessorCount, m->device) != hipSuccess) dev_cu = 256;
-    s->grid_cap = dev_cu * 8;
-    rc = rc ? rc : dalloc(&s->x, (size_t)B * m->ldD);
-    rc = rc ? rc : dalloc(&s->q, (size_t)B * m->H * DK);
-    rc = rc ? rc : dalloc(&s->att, (size_t)B * m->ldD);
-    rc = rc ? rc : dalloc(&s->act, (size_t)B * m->ldF);
     rc = rc ? rc : dalloc(&s->kc, kv);
     rc = rc ? rc : dalloc(&s->vc, kv);
-    rc = rc ? rc : dalloc(&s->part, (size_t)B * m->H * s->nch_cap * (DK + 2));
-    rc = rc ? rc : dalloc(&s->amax_v, (size_t)B * s->grid_cap);
-    rc = rc ? rc : dalloc(&s->amax_i, (size_t)B * s->grid_cap);
+    rc = rc ? rc : dalloc(&s->xa, xa_pairs);
     rc = rc ? rc : dalloc(&s->pos, (size_t)B);
     rc = rc ? rc : dalloc(&s->steps_done, 1);
     rc = rc ? rc : dalloc(&s->err, 1);
-    rc = rc ? rc : dalloc(&s->att_cnt, (size_t)B * m->H);
-    rc = rc ? rc : dalloc(&s->bar, BAR_WORDS);
     rc = rc ? rc : dalloc(&s->n_feed, (size_t)B);
     if (rc) { free_session_buffers(s); delete s; return rc; }
     hipError_t e = hipStreamCreateWithFlags(&s->stream, hipStreamNonBlocking);
     if (e == hipSuccess) e = hipEventCreate(&s->ev0);
     if (e == hipSuccess) e = hipEventCreate(&s->ev1);
-    // padding lanes of the activation rows must stay zero: they meet zero weights
-    if (e == hipSuccess) e = hipMemset(s->x, 0, sizeof(float) * (size_t)B * m->ldD);
-    if (e == hipSuccess) e = hipMemset(s->att, 0, sizeof(float) * (size_t)B * m->ldD);
-    if (e == hipSuccess) e = hipMemset(s->act, 0, sizeof(float) * (size_t)B * m->ldF);
+    // tag 0 is never a step's tag, so a zeroed arena holds no valid value; its
+    // padding columns stay 0.0 for ever (they meet zero weights)
+    if (e == hipSuccess) e = hipMemset(s->xa, 0, sizeof(uint2) * xa_pairs);
     if (e == hipSuccess) e = hipMemset(s->kc, 0, sizeof(float) * kv);
     if (e == hipSuccess) e = hipMemset(s->vc, 0, sizeof(float) * kv);
-    if (e == hipSuccess) e = hipMemset(s->att_cnt, 0, sizeof(unsigned) * (size_t)B * m->H);
     if (e == hipSuccess) e = hipMemset(s->pos, 0, sizeof(int) * (size_t)B);
     if (e != hipSuccess) {
         free_session_buffers(s);
@@ -380,11 +374,7 @@ int dnn_hip_decode(dnn_hip_session *s, const int *feed, int n_feed_all, const in
     dnn_hip_model *m = s->m;
     const int B = s->B;
     if (n_steps <= 0) return fail(DNN_HIP_EINVAL, "n_steps %d", n_steps);
-    // More than NBMAX rows means several batch groups inside one launch.  That
-    // path faulted the GPU once (B=32) and the cause has not been shown, so it
-    // stays switched off until it is.
-    if (B > NBMAX)
-        return fail(DNN_HIP_EINVAL, "batch %d > %d rows per decode launch is disabled", B, NBMAX);
+    if (B > MAXB) return fail(DNN_HIP_EINVAL, "batch %d > %d rows per decode launch", B, MAXB);
     std::vector<int> nf(B);
     int nf_max = 0;
     for (int b = 0; b < B; b++) {
@@ -400,9 +390,13 @@ int dnn_hip_decode(dnn_hip_session *s, const int *feed, int n_feed_all, const in
     for (int b = 0; b < B; b++) {
         if (s->h_pos[b] + n_steps > s->max_seq)
             return fail(DNN_HIP_ERANGE, "row %d: %d cached + %d steps exceeds max_seq %d", b, s->h_pos[b], n_steps, s->max_seq);
-        if (m->rope_cos && s->h_pos[b] + n_steps > m->rope_rows)
+        if (m->rope && s->h_pos[b] + n_steps > m->rope_rows)
             return fail(DNN_HIP_ERANGE, "row %d: position %d beyond the RoPE table (%d rows)", b, s->h_pos[b] + n_steps - 1, m->rope_rows);
     }
+    const int dc = m->ldD / LDALIGN;
+    const int nb = pick_nb(B);
+    const void *kern = decode_kernel_for(nb, dc);
+    if (!kern) return fail(DNN_HIP_EINVAL, "d_model %d: the decode kernels cover d_model <= %d", m->D, 3 * LDALIGN);
     HIP_TRY(hipSetDevice(m->device));
     int rc = grow(&s->feed, &s->feed_cap, (size_t)nf_max * B);
     if (!rc) rc = grow(&s->ids, &s->ids_cap, (size_t)n_steps * B);
@@ -410,45 +404,47 @@ int dnn_hip_decode(dnn_hip_session *s, const int *feed, int n_feed_all, const in
     if (rc) return rc;
     HIP_TRY(hipMemcpyAsync(s->feed, feed, sizeof(int) * (size_t)nf_max * B, hipMemcpyHostToDevice, s->stream));
     HIP_TRY(hipMemcpyAsync(s->n_feed, nf.data(), sizeof(int) * B, hipMemcpyHostToDevice, s->stream));
-    HIP_TRY(hipMemsetAsync(s->bar, 0, sizeof(unsigned long long) * BAR_WORDS, s->stream));
     HIP_TRY(hipMemsetAsync(s->err, 0, sizeof(int), s->stream));
 
-    const int nb = pick_nb(B);
-    const void *kern = decode_kernel_for(nb);
-    const size_t shmem = lds_bytes(nb, std::max(m->ldD, m->ldF));
-    HIP_TRY(hipFuncSetAttribute(kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)shmem));
-    // One workgroup per CU by default: every workgroup must be resident at once
-    // for the grid barriers, and fewer arrivals make each barrier cheaper.  The
-    // launch is a plain one (a cooperative launch would tie the global wave-sync
-    // resource to this process); the barrier's bounded waits keep a launch that
-    // could not be co-scheduled from hanging.
-    int per_cu = 0, n_cu = 0;
+    // One workgroup (8 wavefronts) per CU: the dataflow waits need every
+    // wavefront resident at once.  The launch is a plain one (a cooperative
+    // launch would tie the global wave-sync resource to this process); every
+    // wait is bounded, so a launch that could not be co-scheduled ends with an
+    // error instead of hanging.
+    const size_t shmem = lds_bytes();
+    int per_cu = 0;
     HIP_TRY(hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kern, BLOCK, shmem));
-    HIP_TRY(hipDeviceGetAttribute(&n_cu, hipDeviceAttributeMultiprocessorCount, m->device));
-    if (per_cu <= 0) return fail(DNN_HIP_EDEVICE, "decode kernel does not fit on a CU (shmem %zu)", shmem);
-    int grid = s->grid_req > 0 ? std::min(s->grid_req, per_cu * n_cu) : n_cu;
-    grid = std::min(grid, s->grid_cap);
+    if (per_cu <= 0) return fail(DNN_HIP_EDEVICE, "decode kernel does not fit on a CU");
+    int grid = s->grid_cap;
+    if (s->grid_req > 0) grid = std::min(grid, s->grid_req);
     s->grid = grid;
 
     DecodeArgs a{};
     a.V = m->V; a.D = m->D; a.L = m->L; a.H = m->H; a.F = m->F; a.ldD = m->ldD; a.ldF = m->ldF;
+    a.wts = reinterpret_cast<const float *>(m->arena);
+    a.wts_bytes = (uint32_t)m->arena_bytes;
+    a.embed = (uint32_t)(m->off.embed / sizeof(float));
+    a.lm_bias = (uint32_t)(m->off.lm_bias / sizeof(float));
+    a.g_final = (uint32_t)(m->off.g_final / sizeof(float));
     a.layers = m->d_layers;
-    a.embed = m->embed; a.lm_bias = m->lm_bias; a.g_final = m->g_final; a.eps_final = m->eps_final;
-    a.rope_cos = m->rope_cos; a.rope_sin = m->rope_sin;
-    a.B = B; a.max_seq = s->max_seq; a.nch_cap = s->nch_cap;
-    a.x = s->x; a.q = s->q; a.att = s->att; a.act = s->act; a.kc = s->kc; a.vc = s->vc;
-    a.pos = s->pos; a.part = s->part; a.att_cnt = s->att_cnt; a.amax_v = s->amax_v; a.amax_i = s->amax_i;
-    a.feed = s->feed; a.n_feed = s->n_feed; a.ids = s->ids; a.logits = logits ? s->logits : nullptr;
-    a.n_steps = n_steps; a.eos = eos; a.bar = s->bar; a.err = s->err; a.steps_done = s->steps_done;
+    a.eps_final = m->eps_final;
+    a.rope = m->rope; a.rope_rows = m->rope_rows;
+    a.B = B; a.max_seq = s->max_seq;
+    a.kc = s->kc; a.vc = s->vc; a.xa = s->xa; a.ex = s->ex;
+    a.ex.grid = s->grid_cap;
+    a.pos = s->pos; a.feed = s->feed; a.n_feed = s->n_feed;
+    a.ids = s->ids; a.logits = logits ? s->logits : nullptr;
+    a.n_steps = n_steps; a.eos = eos; a.step0 = s->next_tag; a.err = s->err; a.steps_done = s->steps_done;
+    s->next_tag += (unsigned)n_steps;
     void *kargs[] = {&a};
     HIP_TRY(hipEventRecord(s->ev0, s->stream));
-    HIP_TRY(hipLaunchKernel(kern, dim3(grid), dim3(BLOCK), kargs, (unsigned)shmem, s->stream));
+    HIP_TRY(hipLaunchKernel(kern, dim3(grid), dim3(BLOCK), kargs, shmem, s->stream));
     HIP_TRY(hipEventRecord(s->ev1, s->stream));
     HIP_TRY(hipEventSynchronize(s->ev1));
     HIP_TRY(hipEventElapsedTime(&s->last_ms, s->ev0, s->ev1));
     int done = 0, kerr = 0;
     HIP_TRY(hipMemcpy(&kerr, s->err, sizeof(int), hipMemcpyDeviceToHost));
-    if (kerr) return fail(DNN_HIP_EDEVICE, "decode kernel: a grid barrier timed out (error bits %#x); results discarded", kerr);
+    if (kerr) return fail(DNN_HIP_EDEVICE, "decode kernel: a dependency wait timed out (error bits %#x); results discarded", kerr);
     HIP_TRY(hipMemcpy(&done, s->steps_done, sizeof(int), hipMemcpyDeviceToHost));
     if (ids) HIP_TRY(hipMemcpy(ids, s->ids, sizeof(int) * (size_t)done * B, hipMemcpyDeviceToHost));
     if (logits) HIP_TRY(hipMemcpy(logits, s->logits, sizeof(float) * (size_t)done * B * m->V, hipMemcpyDeviceToHost));

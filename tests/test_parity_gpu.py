@@ -147,10 +147,11 @@ def test_session_bounds_are_errors(c1g):
 
 
 def test_large_batch_is_refused(c1g):
+    """Rows per decode launch are capped at 8; a larger batch is an error at
+    session creation, not a silent split."""
     hm = hip_model(c1g)
-    s = A.HipSession(hm, 9, 16)
-    with pytest.raises(A.HipError, match="disabled"):
-        s.decode(np.zeros((1, 9), dtype=np.int32), 1)
+    with pytest.raises(A.HipError, match="outside"):
+        A.HipSession(hm, 9, 16)
 
 
 @pytest.mark.parametrize("init,seed,pseed,key", [("synthetic", 1, 101, "c1"), ("gpt2", 11, 111, "c1g")])
