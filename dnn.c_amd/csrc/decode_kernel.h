@@ -13,6 +13,7 @@ constexpr int CH = 32;            // cached keys per attention work unit (two ha
 constexpr int DK = 64;            // head dimension the kernels are built for
 constexpr int MAXB = 8;           // batch rows per decode launch
 constexpr int LDALIGN = 256;      // weight rows / activation rows padded to this many floats
+constexpr int FCMAX = 8;          // down-projection input chunks of 256: d_ffn <= 2048
 
 // One transformer block inside the weight arena, as float offsets from its
 // base.  Weight matrices are out-major: row n holds the K inputs of output n,
@@ -37,16 +38,15 @@ struct LayerOff {
 // is the global step id, so a reader knows a value is this step's by its tag
 // and no barrier is needed.  Per layer and batch row:
 //   X1 [ldD]  residual stream after attention    X2 [ldD]  after the FFN
-//   Q, KN, VN [D]  this step's query and new key/value rows (K after RoPE)
+//   Q, KN, VN [D]  this step's query and new key/value rows (after RoPE)
 //   ATT [D]   merged attention heads            ACT [ldF] SwiGLU output
-//   PART [H][nch_cap][DK+2]  split-S attention partials (o[DK], max, sum)
 // then the lm_head argmax partials AMAX [2][B][grid][2] (value, index), double
 // buffered by step parity: a workgroup overwrites its step-t slot at step t+2
 // only after reading every workgroup's step-(t+1) partial, each written after
 // its writer finished reading the step-t partials.
 struct Exch {
-    int ldD, ldF, D, H, nch_cap, B, grid;
-    __host__ __device__ size_t per_row() const { return (size_t)2 * ldD + 4 * (size_t)D + ldF + (size_t)H * nch_cap * (DK + 2); }
+    int ldD, ldF, D, B, grid;
+    __host__ __device__ size_t per_row() const { return (size_t)2 * ldD + 4 * (size_t)D + ldF; }
     __host__ __device__ size_t per_layer() const { return per_row() * B; }
     __host__ __device__ size_t base(int l, int b) const { return per_layer() * l + per_row() * b; }
     __host__ __device__ size_t x1(int l, int b) const { return base(l, b); }
@@ -56,9 +56,6 @@ struct Exch {
     __host__ __device__ size_t vn(int l, int b) const { return q(l, b) + 2 * (size_t)D; }
     __host__ __device__ size_t att(int l, int b) const { return q(l, b) + 3 * (size_t)D; }
     __host__ __device__ size_t act(int l, int b) const { return q(l, b) + 4 * (size_t)D; }
-    __host__ __device__ size_t part(int l, int b, int h, int c) const {
-        return act(l, b) + ldF + ((size_t)h * nch_cap + c) * (DK + 2);
-    }
     __host__ __device__ size_t amax(int L, int par, int b, int g) const {
         return per_layer() * L + (((size_t)par * B + b) * grid + g) * 2;
     }
@@ -75,8 +72,8 @@ struct DecodeArgs {
     const float *rope;      // [2][rope_rows][DK/2]: cos rows, then sin rows; or null
     int rope_rows;
     int B, max_seq;
-    float *kc;              // K^T cache [L][B][H][DK][max_seq]
-    float *vc;              // V cache   [L][B][H][max_seq][DK]
+    float *kc;              // K^T cache [L][B][H][DK][max_seq], then CH*DK floats of padding
+    float *vc;              // V cache   [L][B][H][max_seq][DK], then CH*DK floats of padding
     uint2 *xa;              // exchange arena (Exch layout), pairs
     Exch ex;
     int *pos;               // [B] cached length per row (in/out)
@@ -90,9 +87,14 @@ struct DecodeArgs {
     int *steps_done;
 };
 
-// Dynamic LDS of the decode kernel: per-row token / position / done flags and
-// the per-wavefront argmax scratch.
-inline size_t lds_bytes() { return sizeof(int) * (3 * MAXB + 2 * WPB * MAXB); }
+// Dynamic LDS of the decode kernel (bytes): per-row token / position / done
+// flags, per-wavefront argmax and attention partials, the double-buffered
+// output block of a GEMV round (OUT [2][WPB][2*MAXB]), then the staged rows
+// XS (layer input), AS (attention), X1S and ACTS, nb rows each.
+constexpr int LDS_HEAD_WORDS = 3 * MAXB + 2 * WPB * MAXB + WPB * (DK + 2) + 2 * WPB * 2 * MAXB;
+inline size_t lds_bytes(int nb, int ldD, int ldF) {
+    return (size_t)4 * ((LDS_HEAD_WORDS + 3) / 4 * 4) + (size_t)4 * nb * (3 * (size_t)ldD + ldF);
+}
 
 const void *decode_kernel_for(int nb, int dc);
 

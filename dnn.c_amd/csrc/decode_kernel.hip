@@ -4,9 +4,11 @@
 // (decoder_lm_generate, gpt.c:306-375) for B <= 8 rows at once:
 //
 //   per layer (transformer_block_forward_cached_ex, transformer.c:211-416)
-//     A  rms_norm(x) -> qkv GEMV + bias -> RoPE(q, k) -> Q / KN / VN, K and V cache rows
-//     B  split-S attention over the row's S = pos+1 keys (one 64-key chunk per
-//        wavefront), then a combine of the chunks' (o, max, sum) partials
+//     A  rms_norm(x) -> qkv GEMV + bias -> RoPE(q, k) -> Q / KN / VN
+//     B  attention of one (row, head) per workgroup: each wavefront takes
+//        32-key chunks of the S = pos+1 keys with a running max / sum, the
+//        workgroup merges the wavefronts' (o, max, sum) in LDS; the wavefront
+//        holding position pos appends the new K/V row to the caches
 //     C  out_proj GEMV + bias + residual                      -> X1
 //     D  rms_norm(X1) -> gate/up GEMV + bias -> SwiGLU        -> ACT
 //     E  down GEMV + bias + residual                          -> X2
@@ -15,19 +17,23 @@
 //     G  every workgroup reduces the partials (first index of the maximum,
 //        gpt.c:220-230) and feeds the token to the next step's embedding rows
 //
-// Synchronisation is dataflow, not barriers.  Every value a wavefront produces
-// for others is one 8-byte (value, tag) store with device-coherent (sc1)
-// caching; the tag is the global step id.  A consumer polls the values it needs
-// until all carry this step's tag, so each dependency costs one coherent hop
-// (~0.7 us on MI355X) and no L2 writeback/invalidate is ever issued.  A
-// wavefront issues the weight loads of its next work unit before it polls that
-// unit's inputs, so weight streaming overlaps the wait.
+// Synchronisation is dataflow, not grid barriers.  Every value a wavefront
+// produces for other workgroups is one 8-byte (value, tag) store with
+// device-coherent (sc1) caching; the tag is the global step id.  A workgroup
+// that needs a row (the input of a GEMV phase) stages it into LDS once: its 8
+// wavefronts split the row, poll their parts until every value carries this
+// step's tag, write it to LDS, and meet at a workgroup barrier.  Each
+// dependency costs one coherent hop, no L2 writeback/invalidate is issued, and
+// the row crosses the fabric once per workgroup rather than once per wavefront.
+// A wavefront issues the weight loads of its work unit before the staging
+// poll, so weight streaming overlaps the wait.
 //
 // Weights are out-major (row n = the K inputs of output n, padded to a multiple
 // of 256 floats): each output is one contiguous, coalesced dot product owned by
-// one wavefront.  Every memory access goes through a buffer descriptor sized to
-// its tensor, so the hardware range-checks it (out-of-range loads read 0,
-// stores are dropped).
+// one wavefront; unit u of a phase goes to wavefront u mod (8 * grid), counted
+// workgroup-fastest, so consecutive units land on different CUs.  Every global
+// access goes through a buffer descriptor sized to its tensor, so the hardware
+// range-checks it (out-of-range loads read 0, stores are dropped).
 
 #include <hip/hip_runtime.h>
 #include <stdint.h>
@@ -43,7 +49,6 @@ typedef __amdgpu_buffer_rsrc_t rsrc_t;
 constexpr int CP_NT = 2;        // streaming (non-temporal): weights, read once per step
 constexpr int CP_SC1 = 16;      // device-coherent: everything written inside the launch
 constexpr unsigned SPIN_CAP = 1u << 22;
-constexpr int FCMAX = 8;        // down-projection K chunks held per pass
 
 // Bit reinterpretation through a by-value scalar: clang miscompiles
 // __builtin_bit_cast applied directly to an ext-vector element (q.z reads q.x).
@@ -61,6 +66,12 @@ __device__ __forceinline__ f4 ld4(rsrc_t r, size_t off) {
 template <int CP>
 __device__ __forceinline__ float ld1(rsrc_t r, size_t off) {
     return __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(r, (unsigned)off, 0, CP));
+}
+// voff: per-lane byte offset (VGPR); soff: wave-uniform byte offset (SGPR), so
+// unrolled loads that differ by a uniform stride share one address register
+template <int CP>
+__device__ __forceinline__ float ld1s(rsrc_t r, unsigned voff, unsigned soff) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(r, voff, (int)soff, CP));
 }
 __device__ __forceinline__ void st1(rsrc_t r, size_t off, float v) {
     __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(unsigned, v), r, (unsigned)off, 0, CP_SC1);
@@ -100,28 +111,6 @@ struct Waiter {
     __device__ void reset() { it = 0; }
 };
 
-// One row of n valid values, tagged, starting at pair index `base`: lane holds
-// columns k*256 + 4*lane + j (k < NC, j < 4).  Spins until all carry `tag`.
-template <int NC>
-__device__ __forceinline__ void poll_row(rsrc_t xa, size_t base, int n, unsigned tag, int lane, float *v, Waiter &w) {
-    w.reset();
-    for (;;) {
-        bool ok = true;
-#pragma unroll
-        for (int k = 0; k < NC; k++) {
-#pragma unroll
-            for (int h = 0; h < 2; h++) {
-                const int col = k * 256 + 4 * lane + 2 * h;
-                const u4 q = __builtin_amdgcn_raw_buffer_load_b128(xa, (unsigned)((base + col) * 8), 0, CP_SC1);
-                v[k * 4 + 2 * h] = as_float(q.x);
-                v[k * 4 + 2 * h + 1] = as_float(q.z);
-                ok &= (col >= n || q.y == tag) && (col + 1 >= n || q.w == tag);
-            }
-        }
-        if (__all(ok) || !w.again()) return;
-    }
-}
-
 // A single tagged value per lane at pair index `p` (p < 0: nothing to wait for).
 __device__ __forceinline__ float poll1(rsrc_t xa, long p, unsigned tag, Waiter &w) {
     w.reset();
@@ -132,25 +121,51 @@ __device__ __forceinline__ float poll1(rsrc_t xa, long p, unsigned tag, Waiter &
     }
 }
 
-// rms_norm over lane-held row slices (norm.c:433-440, 466-471):
-// y = (x * rs) * gamma, rs = 1/sqrtf(sum(x^2) * (1/n) + eps).
-template <int NB, int DC>
-__device__ __forceinline__ void rms_rows(float (&x)[NB][DC * 4], rsrc_t rw, size_t g_off, int n, float eps, int lane) {
-    float g[DC * 4];
+// Stage nrows tagged rows (n valid values each, row r at pair index
+// base0 + r * stride) into LDS rows of stride ld.  The rows are cut into
+// 128-value chunks (64 lanes x 2 pairs); chunk c goes to wavefront c % WPB.
+// Columns >= n are left alone (zeroed once at launch).
+template <int NCMAX>
+__device__ __forceinline__ void stage_rows(float *dst, int ld, int n, int nrows, size_t base0, size_t stride,
+                                           rsrc_t xa, unsigned tag, int wid, int lane, Waiter &wt) {
+    const int cpr = (n + 127) / 128, total = nrows * cpr;
+    u4 q[NCMAX];
+    wt.reset();
+    for (;;) {
+        bool ok = true;
 #pragma unroll
-    for (int k = 0; k < DC; k++) {
-        const f4 t = ld4<0>(rw, (g_off + k * 256 + 4 * lane) * 4);
-        g[4 * k] = t.x; g[4 * k + 1] = t.y; g[4 * k + 2] = t.z; g[4 * k + 3] = t.w;
+        for (int i = 0; i < NCMAX; i++) {
+            const int c = wid + i * WPB;
+            if (c >= total) break;
+            const int r = c / cpr, col = (c - r * cpr) * 128 + 2 * lane;
+            q[i] = __builtin_amdgcn_raw_buffer_load_b128(xa, (unsigned)((base0 + r * stride + col) * 8), 0, CP_SC1);
+            const unsigned t0 = q[i].y, t1 = q[i].w;
+            ok &= (col >= n || t0 == tag) && (col + 1 >= n || t1 == tag);
+        }
+        if (__all(ok) || !wt.again()) break;
     }
+#pragma unroll
+    for (int i = 0; i < NCMAX; i++) {
+        const int c = wid + i * WPB;
+        if (c >= total) break;
+        const int r = c / cpr, col = (c - r * cpr) * 128 + 2 * lane;
+        if (col < n) dst[r * ld + col] = as_float(q[i].x);
+        if (col + 1 < n) dst[r * ld + col + 1] = as_float(q[i].z);
+    }
+}
+
+// Reciprocal RMS of nb LDS rows (norm.c:433-440): rs = 1/sqrtf(sum(x^2) * (1/n) + eps).
+template <int NB, int DC>
+__device__ __forceinline__ void rms_lds(const float *xs, int ld, int n, float eps, int lane, float (&rs)[NB]) {
 #pragma unroll
     for (int b = 0; b < NB; b++) {
         float ss = 0.f;
 #pragma unroll
-        for (int i = 0; i < DC * 4; i++) ss += x[b][i] * x[b][i];
-        ss = wave_sum(ss);
-        const float rs = 1.0f / sqrtf(ss * (1.0f / (float)n) + eps);
-#pragma unroll
-        for (int i = 0; i < DC * 4; i++) x[b][i] = (x[b][i] * rs) * g[i];
+        for (int k = 0; k < DC; k++) {
+            const f4 x = *reinterpret_cast<const f4 *>(xs + b * ld + k * 256 + 4 * lane);
+            ss += x.x * x.x + x.y * x.y + x.z * x.z + x.w * x.w;
+        }
+        rs[b] = 1.0f / sqrtf(wave_sum(ss) * (1.0f / (float)n) + eps);
     }
 }
 
@@ -164,70 +179,122 @@ __device__ __forceinline__ void load_rows(f4 (&w)[R][DC], rsrc_t rw, size_t off,
         for (int k = 0; k < DC; k++) w[r][k] = ld4<CP_NT>(rw, (off + (size_t)r * ld + k * 256 + 4 * lane) * 4);
 }
 
-template <int R, int NB, int DC>
-__device__ __forceinline__ void dot_rows(const f4 (&w)[R][DC], const float (&x)[NB][DC * 4], float (&acc)[R][NB]) {
-#pragma unroll
-    for (int r = 0; r < R; r++)
-#pragma unroll
-        for (int b = 0; b < NB; b++) {
-            float s = 0.f;
-#pragma unroll
-            for (int k = 0; k < DC; k++)
-                s += w[r][k].x * x[b][4 * k] + w[r][k].y * x[b][4 * k + 1] + w[r][k].z * x[b][4 * k + 2] + w[r][k].w * x[b][4 * k + 3];
-            acc[r][b] = wave_sum(s);
-        }
-}
-
-// Activation rows of a GEMV input.  `which`: 0 = layer input (the embedding row
-// of this step's token at layer 0, else X2 of the layer below), 1 = X1,
-// 2 = ATT, 3 = X2 of the last layer.
-template <int NB, int DC>
-__device__ __forceinline__ void load_input(float (&x)[NB][DC * 4], const DecodeArgs &a, rsrc_t xa, rsrc_t rw,
-                                           const int *s_tok, int which, int l, unsigned tag, int lane, Waiter &wt) {
+// acc[r][b] = sum_k w[r][k] . y_b[k], y_b = LDS row b, optionally normalised
+// as (x * rs) * gamma (norm.c:466-471) before the product.
+template <int R, int NB, int DC, bool NORM>
+__device__ __forceinline__ void dot_lds(const f4 (&w)[R][DC], const float *xs, int ld, const float (&rs)[NB],
+                                        const f4 (&g)[DC], int lane, float (&acc)[R][NB]) {
 #pragma unroll
     for (int b = 0; b < NB; b++) {
-        const int bb = b < a.B ? b : a.B - 1;
-        if (which == 0 && l == 0) {
+        float s[R];
 #pragma unroll
-            for (int k = 0; k < DC; k++) {
-                const f4 t = ld4<0>(rw, (a.embed + (size_t)s_tok[bb] * a.ldD + k * 256 + 4 * lane) * 4);
-                x[b][4 * k] = t.x; x[b][4 * k + 1] = t.y; x[b][4 * k + 2] = t.z; x[b][4 * k + 3] = t.w;
+        for (int r = 0; r < R; r++) s[r] = 0.f;
+#pragma unroll
+        for (int k = 0; k < DC; k++) {
+            f4 y = *reinterpret_cast<const f4 *>(xs + b * ld + k * 256 + 4 * lane);
+            if (NORM) {
+                y.x = (y.x * rs[b]) * g[k].x; y.y = (y.y * rs[b]) * g[k].y;
+                y.z = (y.z * rs[b]) * g[k].z; y.w = (y.w * rs[b]) * g[k].w;
             }
-        } else {
-            size_t base;
-            if (which == 0) base = a.ex.x2(l - 1, bb);
-            else if (which == 1) base = a.ex.x1(l, bb);
-            else if (which == 2) base = a.ex.att(l, bb);
-            else base = a.ex.x2(a.L - 1, bb);
-            poll_row<DC>(xa, base, a.D, tag, lane, x[b], wt);
+#pragma unroll
+            for (int r = 0; r < R; r++) s[r] += w[r][k].x * y.x + w[r][k].y * y.y + w[r][k].z * y.z + w[r][k].w * y.w;
         }
+#pragma unroll
+        for (int r = 0; r < R; r++) acc[r][b] = wave_sum(s[r]);
     }
+}
+
+// R weight rows of one work unit and their biases, loaded together before the
+// unit's inputs are waited for.
+template <int R, int DC>
+struct RowUnit {
+    f4 w[R][DC];
+    float bias[R];
+};
+template <int R, int DC>
+__device__ __forceinline__ void load_unit(RowUnit<R, DC> &u, rsrc_t rw, size_t woff, int ld, const size_t (&boff)[R], int lane) {
+    load_rows<R, DC>(u.w, rw, woff, ld, lane);
+#pragma unroll
+    for (int r = 0; r < R; r++) u.bias[r] = ld1<0>(rw, boff[r] * 4);
+}
+
+// Output block of one GEMV round of a workgroup: its WPB wavefronts own the
+// consecutive units u0 .. u0+WPB-1, R outputs each, for NB batch rows, and
+// left them in LDS (out[w][b*R + r]).  One wavefront writes them as tagged
+// pairs; consecutive lanes hit consecutive pairs, so every row's block leaves
+// as one coalesced store instead of WPB*R scattered 8-byte ones (scattered
+// single-value stores to shared lines made each hop several times slower).
+template <int R, int NB>
+__device__ __forceinline__ void write_block(const float *out, rsrc_t xa, size_t row0, size_t rstride, int u0, int nu,
+                                            int B, unsigned tag, int lane) {
+    constexpr int PER = WPB * R;
+#pragma unroll
+    for (int i0 = 0; i0 < NB * PER; i0 += WAVE) {
+        const int i = i0 + lane;
+        const int b = i / PER, j = i - b * PER, w = j / R, r = j - w * R;
+        if (i < NB * PER && b < B && u0 + w < nu)
+            put(xa, row0 + b * rstride + (size_t)(u0 + w) * R + r, out[w * NB * R + b * R + r], tag);
+    }
+}
+
+// The layer's offsets as wave-uniform (SGPR) values: loaded once per wave and
+// broadcast, so every address derived from them stays scalar.
+__device__ __forceinline__ LayerOff load_layer(const LayerOff *p) {
+    LayerOff w = *p;
+    auto u = [](uint32_t v) { return (uint32_t)__builtin_amdgcn_readfirstlane((int)v); };
+    auto f = [](float v) { return __builtin_bit_cast(float, __builtin_amdgcn_readfirstlane(__builtin_bit_cast(int, v))); };
+    w.wqkv = u(w.wqkv); w.bqkv = u(w.bqkv); w.wo = u(w.wo); w.bo = u(w.bo);
+    w.g_attn = u(w.g_attn); w.g_ffn = u(w.g_ffn); w.wgu = u(w.wgu); w.bg = u(w.bg);
+    w.bu = u(w.bu); w.wd = u(w.wd); w.bd = u(w.bd);
+    w.eps_attn = f(w.eps_attn); w.eps_ffn = f(w.eps_ffn);
+    return w;
+}
+
+template <int DC>
+__device__ __forceinline__ void load_gamma(f4 (&g)[DC], rsrc_t rw, size_t off, int lane) {
+#pragma unroll
+    for (int k = 0; k < DC; k++) g[k] = ld4<0>(rw, (off + k * 256 + 4 * lane) * 4);
 }
 
 template <int NB, int DC>
 __global__ void __launch_bounds__(BLOCK)
-decode_v2(DecodeArgs a) {
-    extern __shared__ int smem[];
-    int *s_tok = smem;                                          // [MAXB]
+decode_v3(DecodeArgs a) {
+    extern __shared__ float smem[];
+    int *s_tok = reinterpret_cast<int *>(smem);                 // [MAXB]
     int *s_pos = s_tok + MAXB;                                  // [MAXB]
     int *s_done = s_pos + MAXB;                                 // [MAXB]
     float *s_bv = reinterpret_cast<float *>(s_done + MAXB);     // [WPB][MAXB]
     int *s_bi = reinterpret_cast<int *>(s_bv + WPB * MAXB);     // [WPB][MAXB]
+    float *s_part = reinterpret_cast<float *>(s_bi + WPB * MAXB);   // [WPB][DK + 2]
+    float *s_out = s_part + WPB * (DK + 2);                     // [2][WPB][2 * MAXB]
+    const int ldD = a.ldD, ldF = a.ldF;
+    float *xs = smem + (LDS_HEAD_WORDS + 3) / 4 * 4;            // [NB][ldD] layer input (raw)
+    float *as = xs + NB * ldD;                                  // [NB][ldD] attention output
+    float *x1s = as + NB * ldD;                                 // [NB][ldD] X1 (raw)
+    float *acts = x1s + NB * ldD;                               // [NB][ldF] SwiGLU output
 
-    const int tid = threadIdx.x, lane = tid & (WAVE - 1), wid = tid / WAVE;
-    const int gw = blockIdx.x * WPB + wid, nw = gridDim.x * WPB;
-    const int B = a.B, D = a.D, H = a.H, F = a.F, ldD = a.ldD, ldF = a.ldF, V = a.V;
+    const int tid = threadIdx.x;
+    int lane = tid & (WAVE - 1);
+    const int wid = __builtin_amdgcn_readfirstlane(tid / WAVE);
+    const int G = gridDim.x, g0 = blockIdx.x;
+    const int gw = wid * G + g0;                                // workgroup-fastest wave numbering
+    const int nw = G * WPB;
+    const int B = a.B, D = a.D, H = a.H, F = a.F, V = a.V;
+    const int nrows = B < NB ? B : NB;
     Waiter wt{a.err};
 
     const size_t kv_head = (size_t)DK * a.max_seq;              // floats per (layer, row, head)
     const rsrc_t rw = buf(a.wts, a.wts_bytes);
     const rsrc_t xa = buf(a.xa, a.ex.total(a.L) * 8);
-    const rsrc_t rk = buf(a.kc, (size_t)a.L * B * H * kv_head * 4);
-    const rsrc_t rv = buf(a.vc, (size_t)a.L * B * H * kv_head * 4);
+    const size_t kv_bytes = ((size_t)a.L * B * H * kv_head + (size_t)CH * DK) * 4;   // incl. the padding
+    const rsrc_t rk = buf(a.kc, kv_bytes);
+    const rsrc_t rv = buf(a.vc, kv_bytes);
     const size_t sin_off = (size_t)a.rope_rows * (DK / 2) * 4;      // bytes
     const rsrc_t rrope = buf(a.rope, a.rope ? 2 * sin_off : 0);
+    const size_t xstride = a.ex.per_row();
     const float scale = 1.0f / sqrtf((float)DK);
 
+    for (int i = tid; i < NB * (3 * ldD + ldF); i += BLOCK) xs[i] = 0.f;
     for (int b = tid; b < MAXB; b += BLOCK) {
         s_pos[b] = b < B ? a.pos[b] : 0;
         s_done[b] = 0;
@@ -241,88 +308,122 @@ decode_v2(DecodeArgs a) {
         for (int b = tid; b < B; b += BLOCK)
             if (t < a.n_feed[b]) s_tok[b] = a.feed[(size_t)t * B + b];
         __syncthreads();
-        int max_s = 0;
-        for (int b = 0; b < B; b++) max_s = max(max_s, s_pos[b] + 1);
-        const int nch_max = (max_s + CH - 1) / CH;
 
         for (int l = 0; l < a.L; l++) {
-            const LayerOff w = a.layers[l];
+            const LayerOff w = load_layer(a.layers + l);
+            // opaque per layer: keeps the compiler from hoisting every phase's
+            // lane-dependent addresses out of the loops (they would all stay
+            // live for the whole launch and spill)
+            asm volatile("" : "+v"(lane));
 
-            // ---- A: rms_norm -> qkv + bias -> RoPE -> Q / KN / VN and the cache rows
+            // ---- A: rms_norm -> qkv + bias -> RoPE -> Q / KN / VN.  Unit u = rows
+            // (2u, 2u+1) (RoPE pairs stay in one wavefront); the units of round k
+            // of workgroup g are (k*G + g)*WPB + wid, so a workgroup's outputs are
+            // contiguous (Q, KN and VN are adjacent in the exchange row).
             {
-                const int nu = 3 * D / 2;            // RoPE pairs (2k, 2k+1) stay in one wavefront
-                if (gw < nu) {
-                    f4 wr[2][DC];
-                    load_rows<2, DC>(wr, rw, w.wqkv + 2 * (size_t)gw * ldD, ldD, lane);
-                    float x[NB][DC * 4];
-                    load_input<NB, DC>(x, a, xa, rw, s_tok, 0, l, tag, lane, wt);
-                    rms_rows<NB, DC>(x, rw, w.g_attn, D, w.eps_attn, lane);
-                    for (int u = gw;;) {
-                        const int n = 2 * u;
-                        float acc[2][NB];
-                        dot_rows<2, NB, DC>(wr, x, acc);
-                        const int sec = n / D, within = n - sec * D, h = within / DK, j = within - h * DK;
-                        const float b0 = ld1<0>(rw, (w.bqkv + (size_t)n) * 4), b1 = ld1<0>(rw, (w.bqkv + (size_t)n + 1) * 4);
+                constexpr int UP = 2;                // rounds preloaded before the wait
+                const int nu = 3 * D / 2;
+                RowUnit<2, DC> U[UP];
+                float rc[UP], rsn[UP];               // lane b < NB: cos / sin of row b's position
+                f4 g[DC];
+                auto load_a = [&](int k, int u) {
+                    const int n = 2 * u;
+                    const size_t bo[2] = {w.bqkv + (size_t)n, w.bqkv + (size_t)n + 1};
+                    load_unit<2, DC>(U[k], rw, w.wqkv + (size_t)n * ldD, ldD, bo, lane);
+                    const int sec = n / D, j = (n - sec * D) % DK;
+                    rc[k] = 1.f; rsn[k] = 0.f;
+                    if (sec < 2 && a.rope && lane < NB) {
+                        const size_t ti = ((size_t)s_pos[lane < B ? lane : B - 1] * (DK / 2) + j / 2) * 4;
+                        rc[k] = ld1<0>(rrope, ti);
+                        rsn[k] = ld1<0>(rrope, sin_off + ti);
+                    }
+                };
+                auto comp_a = [&](int k, int u, const float (&rs)[NB], float *out) {
+                    const int n = 2 * u;
+                    float acc[2][NB];
+                    dot_lds<2, NB, DC, true>(U[k].w, xs, ldD, rs, g, lane, acc);
+                    const int sec = n / D;
 #pragma unroll
-                        for (int b = 0; b < NB; b++) {
-                            if (b >= B || lane != 0) continue;
-                            float v0 = acc[0][b] + b0, v1 = acc[1][b] + b1;
-                            const int p = s_pos[b];
-                            if (sec < 2 && a.rope) {     // rope.c:28-32
-                                const size_t ti = ((size_t)p * (DK / 2) + j / 2) * 4;
-                                const float c = ld1<0>(rrope, ti), s = ld1<0>(rrope, sin_off + ti);
-                                const float e = v0, o = v1;
-                                v0 = e * c - o * s;
-                                v1 = e * s + o * c;
-                            }
-                            const size_t dst = (sec == 0 ? a.ex.q(l, b) : sec == 1 ? a.ex.kn(l, b) : a.ex.vn(l, b)) + h * DK + j;
-                            put(xa, dst, v0, tag);
-                            put(xa, dst + 1, v1, tag);
+                    for (int b = 0; b < NB; b++) {
+                        float v0 = acc[0][b] + U[k].bias[0], v1 = acc[1][b] + U[k].bias[1];
+                        if (sec < 2 && a.rope) {     // rope.c:28-32
+                            const float c = bcast(rc[k], b), sn = bcast(rsn[k], b);
+                            const float e = v0, o = v1;
+                            v0 = e * c - o * sn;
+                            v1 = e * sn + o * c;
                         }
-                        u += nw;
-                        if (u >= nu) break;
-                        load_rows<2, DC>(wr, rw, w.wqkv + 2 * (size_t)u * ldD, ldD, lane);
+                        if (lane == 0) { out[wid * NB * 2 + b * 2] = v0; out[wid * NB * 2 + b * 2 + 1] = v1; }
+                    }
+                };
+#pragma unroll
+                for (int k = 0; k < UP; k++)
+                    if ((k * G + g0) * WPB + wid < nu) load_a(k, (k * G + g0) * WPB + wid);
+                const bool busy = g0 * WPB < nu;
+                if (busy) load_gamma<DC>(g, rw, w.g_attn, lane);
+                if (l == 0) {
+                    // embedding rows of this step's tokens (embedding.c:79-84)
+                    for (int c = wid; c < nrows * (ldD / 256); c += WPB) {
+                        const int r = c / (ldD / 256), col = (c - r * (ldD / 256)) * 256 + 4 * lane;
+                        *reinterpret_cast<f4 *>(xs + r * ldD + col) = ld4<0>(rw, (a.embed + (size_t)s_tok[r] * ldD + col) * 4);
+                    }
+                } else if (busy) {
+                    stage_rows<NB * 6 / WPB + 1>(xs, ldD, D, nrows, a.ex.x2(l - 1, 0), xstride, xa, tag, wid, lane, wt);
+                }
+                __syncthreads();
+                if (busy) {
+                    float rs[NB];
+                    rms_lds<NB, DC>(xs, ldD, D, w.eps_attn, lane, rs);
+                    for (int k = 0; (k * G + g0) * WPB < nu; k++) {
+                        const int u0 = (k * G + g0) * WPB, u = u0 + wid;
+                        float *out = s_out + (k & 1) * (WPB * 2 * MAXB);
+                        if (u < nu) {
+                            if (k >= UP) load_a(0, u);
+                            comp_a(k < UP ? k : 0, u, rs, out);
+                        }
+                        __syncthreads();
+                        if (wid == 0) write_block<2, NB>(out, xa, a.ex.q(l, 0), xstride, u0, nu, B, tag, lane);
                     }
                 }
             }
 
-            // ---- B: attention, one 32-key chunk of one (row, head) per wavefront.
+            // ---- B: attention of (row b, head h) = workgroup (b*H + h) mod grid.
             // Scores: lanes 0-31 hold dims 0-31, lanes 32-63 dims 32-63 of the
             // chunk's 32 keys (key = j0 + (lane & 31)); P.V: lane = output dim.
-            {
-                const int nu = B * H * nch_max;
+            for (int bh = g0; bh < B * H; bh += G) {
+                const int b = bh / H, h = bh - b * H;
+                const int p = s_pos[b], S = p + 1, nch = (S + CH - 1) / CH;
                 const int half = lane >> 5, kl = lane & 31;
-                for (int u = gw; u < nu; u += nw) {
-                    const int c = u % nch_max, bh = u / nch_max, b = bh / H, h = bh - b * H;
-                    const int p = s_pos[b], S = p + 1, nch = (S + CH - 1) / CH;
-                    if (c >= nch) continue;
+                const size_t head = (((size_t)l * B + b) * H + h) * kv_head;
+                float m_run = -INFINITY, l_run = 0.f, o_run = 0.f;
+                float q = 0.f, kn = 0.f, vn = 0.f;
+                bool have_q = false;
+                for (int c = wid; c < nch; c += WPB) {
                     const int j0 = c * CH, key = j0 + kl;
-                    const size_t head = (((size_t)l * B + b) * H + h) * kv_head;
                     // cached keys (positions < p) of this chunk, issued before the waits
                     // (unconditional loads, then a select: keys >= p hold stale or
                     // neighbouring values, all finite, never used unmasked)
                     float kt[32], vr[CH];
+                    const unsigned kvo = (unsigned)((head + (size_t)(32 * half) * a.max_seq + key) * 4);
+                    const unsigned vvo = (unsigned)((head + (size_t)j0 * DK + lane) * 4);
 #pragma unroll
                     for (int i = 0; i < 32; i++) {
-                        const float t = ld1<CP_SC1>(rk, (head + (size_t)(32 * half + i) * a.max_seq + key) * 4);
-                        kt[i] = key < p ? t : 0.f;
+                        const float tv = ld1s<CP_SC1>(rk, kvo, (unsigned)(i * a.max_seq * 4));
+                        kt[i] = key < p ? tv : 0.f;
                     }
 #pragma unroll
                     for (int jj = 0; jj < CH; jj++) {
-                        const float t = ld1<CP_SC1>(rv, (head + (size_t)(j0 + jj) * DK + lane) * 4);
-                        vr[jj] = j0 + jj < p ? t : 0.f;
+                        const float tv = ld1s<CP_SC1>(rv, vvo, (unsigned)(jj * DK * 4));
+                        vr[jj] = j0 + jj < p ? tv : 0.f;
                     }
-                    const float q = poll1(xa, (long)(a.ex.q(l, b) + h * DK + lane), tag, wt);
+                    if (!have_q) { q = poll1(xa, (long)(a.ex.q(l, b) + h * DK + lane), tag, wt); have_q = true; }
+                    asm volatile("" : "+v"(q));     // no hoisting of the per-half q selects below
                     const bool has_new = p >= j0 && p < j0 + CH;
-                    float kn = 0.f, vn = 0.f;
                     if (has_new) {
                         kn = poll1(xa, (long)(a.ex.kn(l, b) + h * DK + lane), tag, wt);
                         vn = poll1(xa, (long)(a.ex.vn(l, b) + h * DK + lane), tag, wt);
-                    }
-                    if (has_new) {
-                        // the wavefront owning position p appends it to the caches;
-                        // its s_waitcnt before the output store below orders these
-                        // stores before every later step's reads of them
+                        // append position p to the caches; the workgroup barrier
+                        // before the ATT store below waits for these stores, which
+                        // orders them before every later step's reads
                         st1(rk, (head + (size_t)lane * a.max_seq + p) * 4, kn);    // K^T[d][p]
                         st1(rv, (head + (size_t)p * DK + lane) * 4, vn);           // V[p][d]
                     }
@@ -336,187 +437,213 @@ decode_v2(DecodeArgs a) {
                         if (key == p) s = sn;
                     }
                     const bool valid = key < S;
-                    const float m = wave_max(valid ? s : -INFINITY);
-                    const float e = valid ? expf(s - m) : 0.f;
-                    const float lsum = wave_sum(half ? 0.f : e);
+                    const float m_c = wave_max(valid ? s : -INFINITY);
+                    const float m_new = fmaxf(m_run, m_c);
+                    const float e = valid ? expf(s - m_new) : 0.f;
+                    const float fa = expf(m_run - m_new);
                     float o = 0.f;
 #pragma unroll
                     for (int jj = 0; jj < CH; jj++) o += bcast(e, jj) * vr[jj];
-                    if (has_new) {
-                        o += bcast(e, p - j0) * vn;
-                        __builtin_amdgcn_s_waitcnt(0x0f70);     // vmcnt(0): the cache stores are complete
-                    }
-                    if (nch == 1) {
-                        put(xa, a.ex.att(l, b) + h * DK + lane, o / lsum, tag);
-                    } else {
-                        const size_t pp = a.ex.part(l, b, h, c);
-                        put(xa, pp + lane, o, tag);
-                        if (lane == 0) { put(xa, pp + DK, m, tag); put(xa, pp + DK + 1, lsum, tag); }
-                    }
+                    if (has_new) o += bcast(e, p - j0) * vn;
+                    l_run = l_run * fa + wave_sum(half ? 0.f : e);
+                    o_run = o_run * fa + o;
+                    m_run = m_new;
                 }
-                // combine the chunks of each (row, head): max-rescaled sums
-                for (int u = gw; u < B * H; u += nw) {
-                    const int b = u / H, h = u - b * H;
-                    const int S = s_pos[b] + 1, nch = (S + CH - 1) / CH;
-                    if (nch == 1) continue;
-                    float M = -INFINITY, Ls = 0.f, O = 0.f;
-                    for (int c = 0; c < nch; c++) {
-                        const size_t pp = a.ex.part(l, b, h, c);
-                        const float oc = poll1(xa, (long)(pp + lane), tag, wt);
-                        const float mc = poll1(xa, (long)(pp + DK), tag, wt);
-                        const float lc = poll1(xa, (long)(pp + DK + 1), tag, wt);
-                        const float Mn = fmaxf(M, mc);
-                        const float fa = expf(M - Mn), fb = expf(mc - Mn);
-                        O = O * fa + oc * fb;
-                        Ls = Ls * fa + lc * fb;
-                        M = Mn;
+                s_part[wid * (DK + 2) + lane] = o_run;
+                if (lane == 0) { s_part[wid * (DK + 2) + DK] = m_run; s_part[wid * (DK + 2) + DK + 1] = l_run; }
+                __syncthreads();
+                if (wid == 0) {
+                    float M = -INFINITY;
+                    for (int ww = 0; ww < WPB; ww++) M = fmaxf(M, s_part[ww * (DK + 2) + DK]);
+                    float O = 0.f, Ls = 0.f;
+                    for (int ww = 0; ww < WPB; ww++) {
+                        const float mw = s_part[ww * (DK + 2) + DK];
+                        const float f = mw == -INFINITY ? 0.f : expf(mw - M);
+                        O += s_part[ww * (DK + 2) + lane] * f;
+                        Ls += s_part[ww * (DK + 2) + DK + 1] * f;
                     }
                     put(xa, a.ex.att(l, b) + h * DK + lane, O / Ls, tag);
                 }
+                __syncthreads();
             }
 
-            // ---- C: out_proj + bias + residual -> X1
+            // ---- C: out_proj + bias + residual -> X1 (transformer.c:408); unit u =
+            // rows (2u, 2u+1), workgroup-contiguous rounds as in A
             {
+                constexpr int UP = 2;
                 const int nu = D / 2;
-                if (gw < nu) {
-                    f4 wr[2][DC];
-                    load_rows<2, DC>(wr, rw, w.wo + 2 * (size_t)gw * ldD, ldD, lane);
-                    float x[NB][DC * 4];
-                    load_input<NB, DC>(x, a, xa, rw, s_tok, 2, l, tag, lane, wt);
-                    for (int u = gw;;) {
-                        const int n = 2 * u;
-                        float acc[2][NB];
-                        dot_rows<2, NB, DC>(wr, x, acc);
-                        const float bias = ld1<0>(rw, (w.bo + (size_t)n + (lane & 1)) * 4);
+                RowUnit<2, DC> U[UP];
+                f4 g[DC];
+                float rs[NB];
+                auto load_c = [&](int k, int u) {
+                    const size_t bo[2] = {w.bo + 2 * (size_t)u, w.bo + 2 * (size_t)u + 1};
+                    load_unit<2, DC>(U[k], rw, w.wo + 2 * (size_t)u * ldD, ldD, bo, lane);
+                };
+                auto comp_c = [&](int k, int u, float *out) {
+                    float acc[2][NB];
+                    dot_lds<2, NB, DC, false>(U[k].w, as, ldD, rs, g, lane, acc);
+                    if (lane == 0) {
 #pragma unroll
-                        for (int b = 0; b < NB; b++) {
-                            if (b >= B) continue;
-                            // residual in (lanes 0, 1): embedding row at layer 0, else X2 of the layer below
-                            float r = 0.f;
-                            if (l == 0) {
-                                if (lane < 2) r = ld1<0>(rw, (a.embed + (size_t)s_tok[b] * ldD + n + lane) * 4);
-                            } else {
-                                r = poll1(xa, lane < 2 ? (long)(a.ex.x2(l - 1, b) + n + lane) : -1L, tag, wt);
-                            }
-                            const float y = (lane == 0 ? acc[0][b] : acc[1][b]) + bias;
-                            if (lane < 2) put(xa, a.ex.x1(l, b) + n + lane, r + y, tag);   // transformer.c:408
+                        for (int b = 0; b < NB; b++)
+#pragma unroll
+                            for (int r = 0; r < 2; r++)
+                                out[wid * NB * 2 + b * 2 + r] = xs[b * ldD + 2 * u + r] + (acc[r][b] + U[k].bias[r]);
+                    }
+                };
+#pragma unroll
+                for (int k = 0; k < UP; k++)
+                    if ((k * G + g0) * WPB + wid < nu) load_c(k, (k * G + g0) * WPB + wid);
+                const bool busy = g0 * WPB < nu;
+                if (busy)
+                    stage_rows<NB * 6 / WPB + 1>(as, ldD, D, nrows, a.ex.att(l, 0), xstride, xa, tag, wid, lane, wt);
+                __syncthreads();
+                if (busy) {
+                    for (int k = 0; (k * G + g0) * WPB < nu; k++) {
+                        const int u0 = (k * G + g0) * WPB, u = u0 + wid;
+                        float *out = s_out + (k & 1) * (WPB * 2 * MAXB);
+                        if (u < nu) {
+                            if (k >= UP) load_c(0, u);
+                            comp_c(k < UP ? k : 0, u, out);
                         }
-                        u += nw;
-                        if (u >= nu) break;
-                        load_rows<2, DC>(wr, rw, w.wo + 2 * (size_t)u * ldD, ldD, lane);
+                        __syncthreads();
+                        if (wid == 0) write_block<2, NB>(out, xa, a.ex.x1(l, 0), xstride, u0, nu, B, tag, lane);
                     }
                 }
             }
 
-            // ---- D: rms_norm(X1) -> gate/up + bias -> SwiGLU -> ACT  (nn.c:61-78, simd.h:394-397)
+            // ---- D: rms_norm(X1) -> gate/up + bias -> SwiGLU -> ACT  (nn.c:61-78,
+            // simd.h:394-397); unit f = gate row f and up row f
             {
+                constexpr int UP = 2;
                 const int nu = F;
-                if (gw < nu) {
-                    f4 wr[2][DC];
-                    load_rows<2, DC>(wr, rw, w.wgu + 2 * (size_t)gw * ldD, ldD, lane);
-                    float x[NB][DC * 4];
-                    load_input<NB, DC>(x, a, xa, rw, s_tok, 1, l, tag, lane, wt);
-                    rms_rows<NB, DC>(x, rw, w.g_ffn, D, w.eps_ffn, lane);
-                    for (int f = gw;;) {
-                        float acc[2][NB];
-                        dot_rows<2, NB, DC>(wr, x, acc);
-                        const float bgf = ld1<0>(rw, (w.bg + (size_t)f) * 4), bup = ld1<0>(rw, (w.bu + (size_t)f) * 4);
+                RowUnit<2, DC> U[UP];
+                f4 g[DC];
+                auto load_d = [&](int k, int f) {
+                    const size_t bo[2] = {w.bg + (size_t)f, w.bu + (size_t)f};
+                    load_unit<2, DC>(U[k], rw, w.wgu + 2 * (size_t)f * ldD, ldD, bo, lane);
+                };
+                auto comp_d = [&](int k, const float (&rs)[NB], float *out) {
+                    float acc[2][NB];
+                    dot_lds<2, NB, DC, true>(U[k].w, x1s, ldD, rs, g, lane, acc);
+                    if (lane == 0) {
 #pragma unroll
                         for (int b = 0; b < NB; b++) {
-                            if (b >= B || lane != 0) continue;
-                            const float g = acc[0][b] + bgf, up = acc[1][b] + bup;
-                            put(xa, a.ex.act(l, b) + f, (g / (1.0f + expf(-g))) * up, tag);
+                            const float gg = acc[0][b] + U[k].bias[0], up = acc[1][b] + U[k].bias[1];
+                            out[wid * NB + b] = (gg / (1.0f + expf(-gg))) * up;
                         }
-                        f += nw;
-                        if (f >= nu) break;
-                        load_rows<2, DC>(wr, rw, w.wgu + 2 * (size_t)f * ldD, ldD, lane);
+                    }
+                };
+#pragma unroll
+                for (int k = 0; k < UP; k++)
+                    if ((k * G + g0) * WPB + wid < nu) load_d(k, (k * G + g0) * WPB + wid);
+                const bool busy = g0 * WPB < nu;
+                if (busy) load_gamma<DC>(g, rw, w.g_ffn, lane);
+                if (busy || g0 * WPB < D)            // phase E reads X1S for its residual
+                    stage_rows<NB * 6 / WPB + 1>(x1s, ldD, D, nrows, a.ex.x1(l, 0), xstride, xa, tag, wid, lane, wt);
+                __syncthreads();
+                if (busy) {
+                    float rs[NB];
+                    rms_lds<NB, DC>(x1s, ldD, D, w.eps_ffn, lane, rs);
+                    for (int k = 0; (k * G + g0) * WPB < nu; k++) {
+                        const int u0 = (k * G + g0) * WPB, u = u0 + wid;
+                        float *out = s_out + (k & 1) * (WPB * 2 * MAXB);
+                        if (u < nu) {
+                            if (k >= UP) load_d(0, u);
+                            comp_d(k < UP ? k : 0, rs, out);
+                        }
+                        __syncthreads();
+                        if (wid == 0) write_block<1, NB>(out, xa, a.ex.act(l, 0), xstride, u0, nu, B, tag, lane);
                     }
                 }
             }
 
-            // ---- E: down + bias + residual -> X2
+            // ---- E: down + bias + residual -> X2 (transformer.c:415); unit n = row n
             {
                 const int nu = D, FC = ldF / 256;
-                for (int n = gw; n < nu; n += nw) {
-                    float acc[NB];
+                f4 wr[FCMAX];
+                float bdn = 0.f;
+                auto load_down = [&](int n) {
 #pragma unroll
-                    for (int b = 0; b < NB; b++) acc[b] = 0.f;
-                    for (int k0 = 0; k0 < FC; k0 += FCMAX) {
-                        f4 wr[FCMAX];
+                    for (int k = 0; k < FCMAX; k++)
+                        if (k < FC) wr[k] = ld4<CP_NT>(rw, (w.wd + (size_t)n * ldF + k * 256 + 4 * lane) * 4);
+                    bdn = ld1<0>(rw, (w.bd + (size_t)n) * 4);
+                };
+                if (g0 * WPB + wid < nu) load_down(g0 * WPB + wid);
+                const bool busy = g0 * WPB < nu;
+                if (busy)
+                    stage_rows<NB * 16 / WPB + 1>(acts, ldF, F, nrows, a.ex.act(l, 0), xstride, xa, tag, wid, lane, wt);
+                __syncthreads();
+                if (busy) {
+                    for (int k = 0; (k * G + g0) * WPB < nu; k++) {
+                        const int u0 = (k * G + g0) * WPB, n = u0 + wid;
+                        float *out = s_out + (k & 1) * (WPB * 2 * MAXB);
+                        if (n < nu) {
+                            if (k >= 1) load_down(n);
 #pragma unroll
-                        for (int k = 0; k < FCMAX; k++)
-                            if (k0 + k < FC) wr[k] = ld4<CP_NT>(rw, (w.wd + (size_t)n * ldF + (k0 + k) * 256 + 4 * lane) * 4);
+                            for (int b = 0; b < NB; b++) {
+                                float sum = 0.f;
 #pragma unroll
-                        for (int b = 0; b < NB; b++) {
-                            const int bb = b < B ? b : B - 1;
-                            float xv[FCMAX * 4];
-                            wt.reset();
-                            for (;;) {
-                                bool ok = true;
-#pragma unroll
-                                for (int k = 0; k < FCMAX; k++) {
-                                    if (k0 + k >= FC) continue;
-#pragma unroll
-                                    for (int hh = 0; hh < 2; hh++) {
-                                        const int col = (k0 + k) * 256 + 4 * lane + 2 * hh;
-                                        const u4 q = __builtin_amdgcn_raw_buffer_load_b128(
-                                            xa, (unsigned)((a.ex.act(l, bb) + col) * 8), 0, CP_SC1);
-                                        xv[4 * k + 2 * hh] = as_float(q.x);
-                                        xv[4 * k + 2 * hh + 1] = as_float(q.z);
-                                        ok &= (col >= F || q.y == tag) && (col + 1 >= F || q.w == tag);
-                                    }
+                                for (int c = 0; c < FCMAX; c++) {
+                                    if (c >= FC) continue;
+                                    const f4 y = *reinterpret_cast<const f4 *>(acts + b * ldF + c * 256 + 4 * lane);
+                                    sum += wr[c].x * y.x + wr[c].y * y.y + wr[c].z * y.z + wr[c].w * y.w;
                                 }
-                                if (__all(ok) || !wt.again()) break;
+                                sum = wave_sum(sum);
+                                if (lane == 0) out[wid * NB + b] = x1s[b * ldD + n] + (sum + bdn);
                             }
-                            float s = 0.f;
-#pragma unroll
-                            for (int k = 0; k < FCMAX; k++)
-                                if (k0 + k < FC)
-                                    s += wr[k].x * xv[4 * k] + wr[k].y * xv[4 * k + 1] + wr[k].z * xv[4 * k + 2] + wr[k].w * xv[4 * k + 3];
-                            acc[b] += s;
                         }
-                    }
-                    const float bdn = ld1<0>(rw, (w.bd + (size_t)n) * 4);
-#pragma unroll
-                    for (int b = 0; b < NB; b++) {
-                        if (b >= B) continue;
-                        const float y = wave_sum(acc[b]) + bdn;
-                        const float r = poll1(xa, lane == 0 ? (long)(a.ex.x1(l, b) + n) : -1L, tag, wt);
-                        if (lane == 0) put(xa, a.ex.x2(l, b) + n, r + y, tag);        // transformer.c:415
+                        __syncthreads();
+                        if (wid == 0) write_block<1, NB>(out, xa, a.ex.x2(l, 0), xstride, u0, nu, B, tag, lane);
                     }
                 }
             }
         }
 
         // ---- F: final rms_norm -> tied lm_head + bias -> per-workgroup argmax
+        asm volatile("" : "+v"(lane));
         {
+            constexpr int UP = 4;
             float bv[NB];
             int bi[NB];
 #pragma unroll
             for (int b = 0; b < NB; b++) { bv[b] = -INFINITY; bi[b] = 0x7fffffff; }
             const int nu = V / 2;
-            if (gw < nu) {
-                f4 wr[2][DC];
-                load_rows<2, DC>(wr, rw, a.embed + 2 * (size_t)gw * ldD, ldD, lane);
-                float x[NB][DC * 4];
-                load_input<NB, DC>(x, a, xa, rw, s_tok, 3, 0, tag, lane, wt);
-                rms_rows<NB, DC>(x, rw, a.g_final, D, a.eps_final, lane);
-                for (int u = gw;;) {
-                    const int v = 2 * u;
-                    float acc[2][NB];
-                    dot_rows<2, NB, DC>(wr, x, acc);
-                    const float l0b = ld1<0>(rw, (a.lm_bias + (size_t)v) * 4), l1b = ld1<0>(rw, (a.lm_bias + (size_t)v + 1) * 4);
+            RowUnit<2, DC> U[UP];
+            f4 g[DC];
+            auto load_f = [&](int k, int u) {
+                const int v = 2 * u;
+                const size_t bo[2] = {a.lm_bias + (size_t)v, a.lm_bias + (size_t)v + 1};
+                load_unit<2, DC>(U[k], rw, a.embed + (size_t)v * ldD, ldD, bo, lane);
+            };
+            auto comp_f = [&](int k, int u, const float (&rs)[NB]) {
+                const int v = 2 * u;
+                float acc[2][NB];
+                dot_lds<2, NB, DC, true>(U[k].w, xs, ldD, rs, g, lane, acc);
 #pragma unroll
-                    for (int b = 0; b < NB; b++) {
-                        const float l0 = acc[0][b] + l0b, l1 = acc[1][b] + l1b;
-                        if (l0 > bv[b]) { bv[b] = l0; bi[b] = v; }
-                        if (l1 > bv[b]) { bv[b] = l1; bi[b] = v + 1; }
-                        if (a.logits && b < B && lane < 2)
-                            a.logits[((size_t)t * B + b) * V + v + lane] = lane == 0 ? l0 : l1;
-                    }
-                    u += nw;
-                    if (u >= nu) break;
-                    load_rows<2, DC>(wr, rw, a.embed + 2 * (size_t)u * ldD, ldD, lane);
+                for (int b = 0; b < NB; b++) {
+                    const float l0 = acc[0][b] + U[k].bias[0], l1 = acc[1][b] + U[k].bias[1];
+                    if (l0 > bv[b]) { bv[b] = l0; bi[b] = v; }
+                    if (l1 > bv[b]) { bv[b] = l1; bi[b] = v + 1; }
+                    if (a.logits && b < B && lane < 2)
+                        a.logits[((size_t)t * B + b) * V + v + lane] = lane == 0 ? l0 : l1;
+                }
+            };
+#pragma unroll
+            for (int k = 0; k < UP; k++)
+                if (gw + k * nw < nu) load_f(k, gw + k * nw);
+            if (gw < nu) load_gamma<DC>(g, rw, a.g_final, lane);
+            if (g0 < nu)
+                stage_rows<NB * 6 / WPB + 1>(xs, ldD, D, nrows, a.ex.x2(a.L - 1, 0), xstride, xa, tag, wid, lane, wt);
+            __syncthreads();
+            if (gw < nu) {
+                float rs[NB];
+                rms_lds<NB, DC>(xs, ldD, D, a.eps_final, lane, rs);
+#pragma unroll
+                for (int k = 0; k < UP; k++)
+                    if (gw + k * nw < nu) comp_f(k, gw + k * nw, rs);
+                for (int u = gw + UP * nw; u < nu; u += nw) {
+                    load_f(0, u);
+                    comp_f(0, u, rs);
                 }
             }
             if (lane == 0) {
@@ -532,38 +659,43 @@ decode_v2(DecodeArgs a) {
                     const int ii = s_bi[ww * MAXB + tid];
                     if (vv > v || (vv == v && ii < i)) { v = vv; i = ii; }
                 }
-                const size_t pa = a.ex.amax(a.L, t & 1, tid, blockIdx.x);
+                const size_t pa = a.ex.amax(a.L, t & 1, tid, g0);
                 put(xa, pa, v, tag);
                 put(xa, pa + 1, __builtin_bit_cast(float, i), tag);
             }
         }
 
-        // ---- G: every workgroup reduces the partials -> next token (same in all)
-        if (wid == 0) {
-            for (int b = 0; b < B; b++) {
-                float v = -INFINITY;
-                int i = 0x7fffffff;
-                for (int g0 = 0; g0 < (int)gridDim.x; g0 += WAVE) {
-                    const int g = g0 + lane;
-                    const long pv = g < (int)gridDim.x ? (long)a.ex.amax(a.L, t & 1, b, g) : -1L;
-                    const float vv = poll1(xa, pv, tag, wt);
-                    const float iv = poll1(xa, pv >= 0 ? pv + 1 : -1L, tag, wt);
-                    const int ii = __builtin_bit_cast(int, iv);
-                    if (pv >= 0 && (vv > v || (vv == v && ii < i))) { v = vv; i = ii; }
+        // ---- G: every workgroup reduces the partials -> next token (same in all);
+        // wavefront w reduces rows w, w + 8, ...
+        for (int b = wid; b < B; b += WPB) {
+            float v = -INFINITY;
+            int i = 0x7fffffff;
+            for (int gb = 0; gb < G; gb += WAVE) {
+                const int gg = gb + lane;
+                const size_t pa = a.ex.amax(a.L, t & 1, b, gg < G ? gg : 0);
+                u4 q;
+                wt.reset();
+                for (;;) {
+                    q = __builtin_amdgcn_raw_buffer_load_b128(xa, (unsigned)(pa * 8), 0, CP_SC1);
+                    const unsigned t0 = q.y, t1 = q.w;
+                    if (__all(t0 == tag && t1 == tag) || !wt.again()) break;
                 }
+                const float vv = as_float(q.x);
+                const int ii = (int)(unsigned)q.z;
+                if (gg < G && (vv > v || (vv == v && ii < i))) { v = vv; i = ii; }
+            }
 #pragma unroll
-                for (int o = 32; o >= 1; o >>= 1) {
-                    const float vv = __shfl_xor(v, o, WAVE);
-                    const int ii = __shfl_xor(i, o, WAVE);
-                    if (vv > v || (vv == v && ii < i)) { v = vv; i = ii; }
-                }
-                if (lane == 0) {
-                    if (i < 0 || i >= V) i = 0;     // all-NaN row: argmax keeps index 0
-                    s_tok[b] = i;
-                    s_pos[b] += 1;
-                    if (a.eos >= 0 && t >= a.n_feed[b] - 1 && i == a.eos) s_done[b] = 1;
-                    if (blockIdx.x == 0) a.ids[(size_t)t * B + b] = i;
-                }
+            for (int o = 32; o >= 1; o >>= 1) {
+                const float vv = __shfl_xor(v, o, WAVE);
+                const int ii = __shfl_xor(i, o, WAVE);
+                if (vv > v || (vv == v && ii < i)) { v = vv; i = ii; }
+            }
+            if (lane == 0) {
+                if (i < 0 || i >= V) i = 0;     // all-NaN row: argmax keeps index 0
+                s_tok[b] = i;
+                s_pos[b] += 1;
+                if (a.eos >= 0 && t >= a.n_feed[b] - 1 && i == a.eos) s_done[b] = 1;
+                if (g0 == 0) a.ids[(size_t)t * B + b] = i;
             }
         }
         __syncthreads();
@@ -573,18 +705,18 @@ decode_v2(DecodeArgs a) {
             if (all) { t++; break; }
         }
     }
-    if (blockIdx.x == 0 && tid < B) a.pos[tid] = s_pos[tid];
-    if (blockIdx.x == 0 && tid == 0) *a.steps_done = t;
+    if (g0 == 0 && tid < B) a.pos[tid] = s_pos[tid];
+    if (g0 == 0 && tid == 0) *a.steps_done = t;
 }
 
-#define DNNHIP_INST(NB, DC) template __global__ void decode_v2<NB, DC>(DecodeArgs);
+#define DNNHIP_INST(NB, DC) template __global__ void decode_v3<NB, DC>(DecodeArgs);
 DNNHIP_INST(1, 1) DNNHIP_INST(1, 2) DNNHIP_INST(1, 3)
 DNNHIP_INST(2, 1) DNNHIP_INST(2, 2) DNNHIP_INST(2, 3)
 DNNHIP_INST(4, 1) DNNHIP_INST(4, 2) DNNHIP_INST(4, 3)
 DNNHIP_INST(8, 1) DNNHIP_INST(8, 2) DNNHIP_INST(8, 3)
 
 const void *decode_kernel_for(int nb, int dc) {
-#define DNNHIP_PICK(NB, DC) if (nb == NB && dc == DC) return reinterpret_cast<const void *>(&decode_v2<NB, DC>);
+#define DNNHIP_PICK(NB, DC) if (nb == NB && dc == DC) return reinterpret_cast<const void *>(&decode_v3<NB, DC>);
     DNNHIP_PICK(1, 1) DNNHIP_PICK(1, 2) DNNHIP_PICK(1, 3)
     DNNHIP_PICK(2, 1) DNNHIP_PICK(2, 2) DNNHIP_PICK(2, 3)
     DNNHIP_PICK(4, 1) DNNHIP_PICK(4, 2) DNNHIP_PICK(4, 3)

@@ -54,7 +54,7 @@ struct dnn_hip_model {
 
 struct dnn_hip_session {
     dnn_hip_model *m;
-    int B, max_seq, nch_cap;
+    int B, max_seq;
     hipStream_t stream = nullptr;
     hipEvent_t ev0 = nullptr, ev1 = nullptr;
     float *kc = nullptr, *vc = nullptr;       // K^T [L][B][H][DK][max_seq], V [L][B][H][max_seq][DK]
@@ -197,6 +197,7 @@ int dnn_hip_model_create(int V, int D, int L, int H, int dk, int F, const float 
     if (dk != DK) return fail(DNN_HIP_EINVAL, "the decode kernels are built for d_k=%d (got %d)", DK, dk);
     if (D % 2 || V % 2) return fail(DNN_HIP_EINVAL, "d_model and vocab_size must be even");
     if (D > 3 * LDALIGN) return fail(DNN_HIP_EINVAL, "d_model %d: the decode kernels cover d_model <= %d", D, 3 * LDALIGN);
+    if (F > FCMAX * LDALIGN) return fail(DNN_HIP_EINVAL, "d_ffn %d: the decode kernels cover d_ffn <= %d", F, FCMAX * LDALIGN);
     int dev = 0;
     HIP_TRY(hipGetDevice(&dev));
     auto *m = new dnn_hip_model();
@@ -284,13 +285,14 @@ int dnn_hip_session_create(dnn_hip_model *m, int B, int max_seq, dnn_hip_session
     s->m = m;
     s->B = B;
     s->max_seq = max_seq;
-    s->nch_cap = (max_seq + CH - 1) / CH;
     s->h_pos.assign(B, 0);
     int n_cu = 0;
     if (hipDeviceGetAttribute(&n_cu, hipDeviceAttributeMultiprocessorCount, m->device) != hipSuccess || n_cu <= 0) n_cu = 256;
     s->grid_cap = n_cu;
-    s->ex = Exch{m->ldD, m->ldF, m->D, m->H, s->nch_cap, B, s->grid_cap};
-    const size_t kv = (size_t)m->L * B * m->H * max_seq * DK;
+    s->ex = Exch{m->ldD, m->ldF, m->D, B, s->grid_cap};
+    // + CH*DK floats of zeroed padding: attention reads whole 32-key chunks,
+    // and the rows past max_seq of the last head must stay inside the allocation
+    const size_t kv = (size_t)m->L * B * m->H * max_seq * DK + (size_t)CH * DK;
     const size_t xa_pairs = s->ex.total(m->L);
     if (kv * sizeof(float) >= 0x7fffffffu || xa_pairs * 8 >= 0x7fffffffu) {
         delete s;
@@ -411,7 +413,12 @@ int dnn_hip_decode(dnn_hip_session *s, const int *feed, int n_feed_all, const in
     // launch would tie the global wave-sync resource to this process); every
     // wait is bounded, so a launch that could not be co-scheduled ends with an
     // error instead of hanging.
-    const size_t shmem = lds_bytes();
+    const size_t shmem = lds_bytes(nb, m->ldD, m->ldF);
+    int lds_max = 0;
+    HIP_TRY(hipDeviceGetAttribute(&lds_max, hipDeviceAttributeMaxSharedMemoryPerBlock, m->device));
+    if (shmem > (size_t)lds_max)
+        return fail(DNN_HIP_EINVAL, "decode kernel needs %zu B of LDS for %d rows, the device has %d", shmem, nb, lds_max);
+    HIP_TRY(hipFuncSetAttribute(kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)shmem));
     int per_cu = 0;
     HIP_TRY(hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kern, BLOCK, shmem));
     if (per_cu <= 0) return fail(DNN_HIP_EDEVICE, "decode kernel does not fit on a CU");
