@@ -106,6 +106,18 @@ def step_bytes(V, D, Ly, F, positions, B):
     return total
 
 
+def measured_traffic(cfg, positions):
+    """HBM bytes of this launch from the committed rocprofv3 --pmc summary of
+    the same workload (profiles/traffic_<cfg>.json: FETCH_SIZE + WRITE_SIZE
+    per step, scaled by a copy kernel of known size), or None if absent."""
+    path = os.path.join(ROOT, "profiles", "traffic_%s.json" % cfg)
+    if not os.path.exists(path):
+        return None
+    with open(path) as f:
+        t = json.load(f)
+    return int(round(t["hbm_bytes_per_step"] * len(positions)))
+
+
 def cpu_baseline(cfg, budget_tokens):
     """The reference itself (oracle/_ref/ref_bench, built from its sources), one
     thread, on a bounded sample of the same model: 4-token prompt, then
@@ -140,7 +152,10 @@ def main():
     ap.add_argument("--steps", type=int, default=512)
     ap.add_argument("--warmup", type=int, default=16)
     ap.add_argument("--config", default="c2", choices=sorted(CONFIGS))
-    ap.add_argument("--grid", type=int, default=0, help="persistent-kernel workgroups (0 = cooperative max)")
+    ap.add_argument("--grid", type=int, default=0, help="persistent-kernel workgroups (0 = one per CU)")
+    ap.add_argument("--copy-probe", type=int, default=0, metavar="MIB",
+                    help="after the timed decode, copy a MIB-sized device buffer 3 times (a plain copy kernel of "
+                         "known size, the scale for rocprofv3 FETCH_SIZE / WRITE_SIZE counters)")
     ap.add_argument("--cpu-tokens", type=int, default=24)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     args = ap.parse_args()
@@ -190,9 +205,19 @@ def main():
         "device_ms_per_step": round(dev_ms / args.steps, 5),
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": 8000.0, "unit": "GB/s",
                      "frac": round(achieved / 8000.0, 4), "traffic": None,
-                     "kernel": "dnnhip::decode_persistent (one launch = %d steps)" % args.steps,
+                     "kernel": "dnnhip::decode_v3<NB,DC> (one persistent launch = %d steps)" % args.steps,
                      "algorithmic_bytes_per_launch": nbytes},
     }
+    traffic = measured_traffic(args.config, positions)
+    if traffic is not None:
+        line["roofline"]["traffic"] = traffic
+    if args.copy_probe:
+        import torch
+        x = torch.empty(args.copy_probe << 18, dtype=torch.float32, device="cuda").fill_(1.0)
+        y = torch.empty_like(x)
+        for _ in range(3):
+            y.copy_(x)
+        torch.cuda.synchronize()
     if not args.no_cpu_baseline:
         line["cpu_baseline"] = cpu_baseline(args.config, args.cpu_tokens)
     print(json.dumps(line))

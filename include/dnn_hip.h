@@ -80,8 +80,10 @@ int dnn_hip_model_rope(dnn_hip_model *m, const float *cos_table,
 
 int dnn_hip_model_destroy(dnn_hip_model *m);
 
-/* A decode session: per-layer KV rings [B][H][max_seq][d_k] in HBM plus the
- * activation arena.  Every row starts empty. */
+/* A decode session: the per-layer KV caches of `batch` rows in HBM (K stored
+ * transposed, [L][B][H][d_k][max_seq]; V as [L][B][H][max_seq][d_k]) plus the
+ * exchange arena of the decode kernel.  Every row starts empty.
+ * 1 <= batch <= 8. */
 int dnn_hip_session_create(dnn_hip_model *m, int batch, int max_seq,
                            dnn_hip_session **out);
 /* Empties every row (lengths back to 0). */
@@ -98,8 +100,7 @@ int dnn_hip_session_destroy(dnn_hip_session *s);
  * (nullable) receives the [n_steps][batch][V] rows.  With eos >= 0 the loop
  * ends early once every row has produced eos in its greedy part; *steps_done
  * (nullable) gets the number of steps run.  Requires n_feed >= 1 per row and
- * length + n_steps <= max_seq (and <= RoPE rows).  At most 8 rows per call for
- * now (larger batches return DNN_HIP_EINVAL). */
+ * length + n_steps <= max_seq (and <= RoPE rows). */
 int dnn_hip_decode(dnn_hip_session *s, const int *feed, int n_feed_all,
                    const int *n_feed, int n_steps, int eos, int *ids,
                    float *logits, int *steps_done);
@@ -115,7 +116,8 @@ int dnn_hip_generate(dnn_hip_model *m, const int *prompt, int n_prompt,
 int dnn_hip_session_last_ms(dnn_hip_session *s, float *ms);
 
 /* Number of workgroups the persistent decode kernel runs with on this session
- * (0 = choose the cooperative maximum) -- a tuning knob. */
+ * (0 = one per compute unit, the default; larger values are capped there) --
+ * a tuning knob. */
 int dnn_hip_session_set_grid(dnn_hip_session *s, int n_workgroups);
 /* Workgroups the last dnn_hip_decode launch on this session used. */
 int dnn_hip_session_grid(dnn_hip_session *s, int *n_workgroups);
