@@ -96,6 +96,17 @@ inline size_t lds_bytes(int nb, int ldD, int ldF) {
     return (size_t)4 * ((LDS_HEAD_WORDS + 3) / 4 * 4) + (size_t)4 * nb * (3 * (size_t)ldD + ldF);
 }
 
+// The lookahead kernel (one or two rows): LDS head, then XS, AS, X1S [nb][ldD],
+// ACTS [nb][ldF], the 2L+1 RMSNorm gammas [ldD], their epsilons, the layer
+// offset table and the RoPE entries of the A units.
+constexpr int LDS4_HEAD_WORDS = (3 * MAXB + 2 * WPB * MAXB + WPB * (DK + 2) + 3 * WPB * 2 * MAXB + 3 * DK +
+                                 WPB * 3 * MAXB * 2 + 3) / 4 * 4;
+inline size_t lds4_bytes(int nb, int ldD, int ldF, int L) {
+    return (size_t)4 * LDS4_HEAD_WORDS + (size_t)4 * nb * (3 * (size_t)ldD + ldF) + (size_t)4 * (2 * L + 1) * ldD +
+           (size_t)4 * (2 * L + 1) + sizeof(LayerOff) * (size_t)L;
+}
+
 const void *decode_kernel_for(int nb, int dc);
+const void *decode_lookahead_for(int nb, int dc);
 
 }  // namespace dnnhip

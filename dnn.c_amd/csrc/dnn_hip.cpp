@@ -2,6 +2,7 @@
 // parameters, KV rings, and the launch of the persistent decode kernel.
 #include <hip/hip_runtime.h>
 #include <algorithm>
+#include <cstdlib>
 #include <cstdarg>
 #include <cstdio>
 #include <cstring>
@@ -67,6 +68,8 @@ struct dnn_hip_session {
     size_t logits_cap = 0;
     int grid_req = 0, grid = 0, grid_cap = 0;
     unsigned next_tag = 1;                    // tags only grow: stale values never match
+    int kernel_pref = 0;                      // 0: automatic, 3: always decode_v3
+    int kernel_used = 0;                      // 3 or 4: the kernel of the last launch
     float last_ms = 0.f;
     std::vector<int> h_pos;
 };
@@ -286,6 +289,7 @@ int dnn_hip_session_create(dnn_hip_model *m, int B, int max_seq, dnn_hip_session
     s->B = B;
     s->max_seq = max_seq;
     s->h_pos.assign(B, 0);
+    if (const char *k = getenv("DNN_HIP_DECODE_KERNEL")) s->kernel_pref = atoi(k);   // "3": force decode_v3
     int n_cu = 0;
     if (hipDeviceGetAttribute(&n_cu, hipDeviceAttributeMultiprocessorCount, m->device) != hipSuccess || n_cu <= 0) n_cu = 256;
     s->grid_cap = n_cu;
@@ -364,6 +368,12 @@ int dnn_hip_session_grid(dnn_hip_session *s, int *grid) {
     return DNN_HIP_OK;
 }
 
+int dnn_hip_session_kernel(dnn_hip_session *s, int *which) {
+    if (!s || !which) return fail(DNN_HIP_EINVAL, "NULL argument");
+    *which = s->kernel_used;
+    return DNN_HIP_OK;
+}
+
 int dnn_hip_session_last_ms(dnn_hip_session *s, float *ms) {
     if (!s || !ms) return fail(DNN_HIP_EINVAL, "NULL argument");
     *ms = s->last_ms;
@@ -397,9 +407,28 @@ int dnn_hip_decode(dnn_hip_session *s, const int *feed, int n_feed_all, const in
     }
     const int dc = m->ldD / LDALIGN;
     const int nb = pick_nb(B);
-    const void *kern = decode_kernel_for(nb, dc);
-    if (!kern) return fail(DNN_HIP_EINVAL, "d_model %d: the decode kernels cover d_model <= %d", m->D, 3 * LDALIGN);
     HIP_TRY(hipSetDevice(m->device));
+    int lds_max = 0;
+    HIP_TRY(hipDeviceGetAttribute(&lds_max, hipDeviceAttributeMaxSharedMemoryPerBlock, m->device));
+    int grid = s->grid_cap;
+    if (s->grid_req > 0) grid = std::min(grid, s->grid_req);
+    // One or two rows: the lookahead kernel when its schedule fits (every GEMV
+    // round in at most 3 slots of the grid's non-attention workgroups, and its
+    // LDS); otherwise, and for more rows, decode_v3.
+    const void *kern = nullptr;
+    size_t shmem = 0;
+    const int rounds = (m->D + 6) / 7 + (3 * m->D / 2 + 6) / 7 + (m->D / 2 + 6) / 7 + (m->F + 6) / 7;
+    if (nb <= 2 && s->kernel_pref != 3 && grid > B * m->H && rounds <= 3 * (grid - B * m->H) &&
+        lds4_bytes(nb, m->ldD, m->ldF, m->L) <= (size_t)lds_max) {
+        kern = decode_lookahead_for(nb, dc);
+        shmem = lds4_bytes(nb, m->ldD, m->ldF, m->L);
+    }
+    if (!kern) {
+        kern = decode_kernel_for(nb, dc);
+        shmem = lds_bytes(nb, m->ldD, m->ldF);
+    }
+    if (!kern) return fail(DNN_HIP_EINVAL, "d_model %d: the decode kernels cover d_model <= %d", m->D, 3 * LDALIGN);
+    s->kernel_used = kern == decode_kernel_for(nb, dc) ? 3 : 4;
     int rc = grow(&s->feed, &s->feed_cap, (size_t)nf_max * B);
     if (!rc) rc = grow(&s->ids, &s->ids_cap, (size_t)n_steps * B);
     if (!rc && logits) rc = grow(&s->logits, &s->logits_cap, (size_t)n_steps * B * m->V);
@@ -413,17 +442,12 @@ int dnn_hip_decode(dnn_hip_session *s, const int *feed, int n_feed_all, const in
     // launch would tie the global wave-sync resource to this process); every
     // wait is bounded, so a launch that could not be co-scheduled ends with an
     // error instead of hanging.
-    const size_t shmem = lds_bytes(nb, m->ldD, m->ldF);
-    int lds_max = 0;
-    HIP_TRY(hipDeviceGetAttribute(&lds_max, hipDeviceAttributeMaxSharedMemoryPerBlock, m->device));
     if (shmem > (size_t)lds_max)
         return fail(DNN_HIP_EINVAL, "decode kernel needs %zu B of LDS for %d rows, the device has %d", shmem, nb, lds_max);
     HIP_TRY(hipFuncSetAttribute(kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)shmem));
     int per_cu = 0;
     HIP_TRY(hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kern, BLOCK, shmem));
     if (per_cu <= 0) return fail(DNN_HIP_EDEVICE, "decode kernel does not fit on a CU");
-    int grid = s->grid_cap;
-    if (s->grid_req > 0) grid = std::min(grid, s->grid_req);
     s->grid = grid;
 
     DecodeArgs a{};

@@ -23,7 +23,7 @@ HIP_SYMBOLS = [
     "dnn_hip_model_rope", "dnn_hip_model_destroy", "dnn_hip_session_create",
     "dnn_hip_session_reset", "dnn_hip_session_lengths", "dnn_hip_session_destroy",
     "dnn_hip_decode", "dnn_hip_generate", "dnn_hip_session_last_ms", "dnn_hip_session_set_grid",
-    "dnn_hip_session_grid",
+    "dnn_hip_session_grid", "dnn_hip_session_kernel",
 ]
 
 
@@ -56,6 +56,7 @@ def hip():
         L.dnn_hip_session_last_ms.argtypes = [C.c_void_p, f32p]
         L.dnn_hip_session_set_grid.argtypes = [C.c_void_p, C.c_int]
         L.dnn_hip_session_grid.argtypes = [C.c_void_p, i32p]
+        L.dnn_hip_session_kernel.argtypes = [C.c_void_p, i32p]
         _hip = L
     return _hip
 
@@ -120,6 +121,12 @@ class HipSession:
         g = C.c_int()
         check(hip().dnn_hip_session_grid(self.ptr, C.byref(g)))
         return g.value
+
+    def kernel(self):
+        """3 or 4: the decode kernel of the last decode() call."""
+        k = C.c_int()
+        check(hip().dnn_hip_session_kernel(self.ptr, C.byref(k)))
+        return k.value
 
     def set_grid(self, n):
         check(hip().dnn_hip_session_set_grid(self.ptr, n))

@@ -121,6 +121,11 @@ int dnn_hip_session_last_ms(dnn_hip_session *s, float *ms);
 int dnn_hip_session_set_grid(dnn_hip_session *s, int n_workgroups);
 /* Workgroups the last dnn_hip_decode launch on this session used. */
 int dnn_hip_session_grid(dnn_hip_session *s, int *n_workgroups);
+/* Which decode kernel the last dnn_hip_decode launch used: 4 = the layer-
+ * lookahead kernel (1-2 rows), 3 = the general one (up to 8 rows).  The
+ * environment variable DNN_HIP_DECODE_KERNEL=3, read at session creation,
+ * forces the general kernel. */
+int dnn_hip_session_kernel(dnn_hip_session *s, int *which);
 
 #ifdef __cplusplus
 }

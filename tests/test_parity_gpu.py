@@ -119,6 +119,24 @@ def test_batch_rows_match_independent_runs(c1g, B):
     assert list(s.lengths()) == [steps] * B
 
 
+@pytest.mark.parametrize("B", [1, 2])
+def test_lookahead_kernel_equals_general_kernel(golden, c2, monkeypatch, B):
+    """One and two rows run the layer-lookahead kernel; its logits must equal
+    the general kernel's bit for bit (same arithmetic, different schedule)."""
+    _, hm = c2
+    toks = np.array(golden["c2_tokens"][:48], dtype=np.int32)
+    feed = np.stack([toks] * B, axis=1) if B > 1 else toks
+    s4 = A.HipSession(hm, B, 64)
+    ids4, lg4 = s4.decode(feed, 48, want_logits=True)
+    assert s4.kernel() == 4
+    monkeypatch.setenv("DNN_HIP_DECODE_KERNEL", "3")
+    s3 = A.HipSession(hm, B, 64)
+    ids3, lg3 = s3.decode(feed, 48, want_logits=True)
+    assert s3.kernel() == 3
+    assert np.array_equal(ids4, ids3)
+    assert np.array_equal(lg4.view(np.uint32), lg3.view(np.uint32))
+
+
 def test_eos_stops_generation():
     """A bias pushing id 258 to the top makes the first generated token EOS: the
     run stops there (gpt.c:339), on the device as in the oracle."""
