@@ -12,6 +12,7 @@ constexpr int WPB = BLOCK / WAVE;
 constexpr int CH = 32;            // cached keys per attention work unit (two half-waves per key)
 constexpr int DK = 64;            // head dimension the kernels are built for
 constexpr int MAXB = 8;           // batch rows per decode launch
+constexpr int MAX_ROWS = 64;      // rows per session (groups of MAXB run in turn)
 constexpr int LDALIGN = 256;      // weight rows / activation rows padded to this many floats
 constexpr int FCMAX = 8;          // down-projection input chunks of 256: d_ffn <= 2048
 

@@ -169,10 +169,12 @@ decode_v3(DecodeArgs a) {
                 }
             }
 
-            // ---- B: attention of (row b, head h) = workgroup (b*H + h) mod grid.
+            // ---- B: attention of (row b, head h) = workgroup G-1-((b*H + h) mod G):
+            // the last workgroups, which hold no phase-A units for the model
+            // shapes served, so their K/V loads start as the layer starts.
             // Scores: lanes 0-31 hold dims 0-31, lanes 32-63 dims 32-63 of the
             // chunk's 32 keys (key = j0 + (lane & 31)); P.V: lane = output dim.
-            for (int bh = g0; bh < B * H; bh += G) {
+            for (int bh = G - 1 - g0; bh < B * H; bh += G) {
                 const int b = bh / H, h = bh - b * H;
                 const int p = s_pos[b], S = p + 1, nch = (S + CH - 1) / CH;
                 const int half = lane >> 5, kl = lane & 31;

@@ -68,10 +68,13 @@ struct dnn_hip_session {
     size_t logits_cap = 0;
     int grid_req = 0, grid = 0, grid_cap = 0;
     unsigned next_tag = 1;                    // tags only grow: stale values never match
-    int kernel_pref = 0;                      // 0: automatic, 3: always decode_v3
+    int kernel_pref = 0;                      // 4: the lookahead kernel where it applies
     int kernel_used = 0;                      // 3 or 4: the kernel of the last launch
     float last_ms = 0.f;
     std::vector<int> h_pos;
+    // more than MAXB rows: consecutive groups of at most MAXB rows, each its own
+    // session, run one after another by dnn_hip_decode
+    std::vector<dnn_hip_session *> groups;
 };
 
 namespace {
@@ -281,15 +284,29 @@ int dnn_hip_model_destroy(dnn_hip_model *m) {
 int dnn_hip_session_create(dnn_hip_model *m, int B, int max_seq, dnn_hip_session **out) {
     if (!m || !out) return fail(DNN_HIP_EINVAL, "NULL argument");
     *out = nullptr;
-    if (B <= 0 || B > MAXB) return fail(DNN_HIP_EINVAL, "batch %d outside [1,%d]", B, MAXB);
+    if (B <= 0 || B > MAX_ROWS) return fail(DNN_HIP_EINVAL, "batch %d outside [1,%d]", B, MAX_ROWS);
     if (max_seq <= 0) return fail(DNN_HIP_EINVAL, "max_seq %d", max_seq);
     HIP_TRY(hipSetDevice(m->device));
+    if (B > MAXB) {
+        auto *s = new dnn_hip_session();
+        s->m = m;
+        s->B = B;
+        s->max_seq = max_seq;
+        for (int r0 = 0; r0 < B; r0 += MAXB) {
+            dnn_hip_session *g = nullptr;
+            const int rc = dnn_hip_session_create(m, std::min(MAXB, B - r0), max_seq, &g);
+            if (rc) { dnn_hip_session_destroy(s); return rc; }
+            s->groups.push_back(g);
+        }
+        *out = s;
+        return DNN_HIP_OK;
+    }
     auto *s = new dnn_hip_session();
     s->m = m;
     s->B = B;
     s->max_seq = max_seq;
     s->h_pos.assign(B, 0);
-    if (const char *k = getenv("DNN_HIP_DECODE_KERNEL")) s->kernel_pref = atoi(k);   // "3": force decode_v3
+    if (const char *k = getenv("DNN_HIP_DECODE_KERNEL")) s->kernel_pref = atoi(k);   // "4": lookahead kernel
     int n_cu = 0;
     if (hipDeviceGetAttribute(&n_cu, hipDeviceAttributeMultiprocessorCount, m->device) != hipSuccess || n_cu <= 0) n_cu = 256;
     s->grid_cap = n_cu;
@@ -332,6 +349,11 @@ int dnn_hip_session_create(dnn_hip_model *m, int B, int max_seq, dnn_hip_session
 
 int dnn_hip_session_reset(dnn_hip_session *s) {
     if (!s) return fail(DNN_HIP_EINVAL, "session is NULL");
+    for (dnn_hip_session *g : s->groups) {
+        const int rc = dnn_hip_session_reset(g);
+        if (rc) return rc;
+    }
+    if (!s->groups.empty()) return DNN_HIP_OK;
     HIP_TRY(hipSetDevice(s->m->device));
     HIP_TRY(hipMemset(s->pos, 0, sizeof(int) * (size_t)s->B));
     std::fill(s->h_pos.begin(), s->h_pos.end(), 0);
@@ -340,12 +362,21 @@ int dnn_hip_session_reset(dnn_hip_session *s) {
 
 int dnn_hip_session_lengths(dnn_hip_session *s, int *lens) {
     if (!s || !lens) return fail(DNN_HIP_EINVAL, "NULL argument");
+    if (!s->groups.empty()) {
+        int r0 = 0;
+        for (dnn_hip_session *g : s->groups) {
+            dnn_hip_session_lengths(g, lens + r0);
+            r0 += g->B;
+        }
+        return DNN_HIP_OK;
+    }
     memcpy(lens, s->h_pos.data(), sizeof(int) * (size_t)s->B);
     return DNN_HIP_OK;
 }
 
 int dnn_hip_session_destroy(dnn_hip_session *s) {
     if (!s) return DNN_HIP_OK;
+    for (dnn_hip_session *g : s->groups) dnn_hip_session_destroy(g);
     (void)hipSetDevice(s->m->device);
     if (s->stream) (void)hipStreamSynchronize(s->stream);
     free_session_buffers(s);
@@ -358,19 +389,20 @@ int dnn_hip_session_destroy(dnn_hip_session *s) {
 
 int dnn_hip_session_set_grid(dnn_hip_session *s, int n) {
     if (!s || n < 0) return fail(DNN_HIP_EINVAL, "bad argument");
+    for (dnn_hip_session *g : s->groups) g->grid_req = n;
     s->grid_req = n;
     return DNN_HIP_OK;
 }
 
 int dnn_hip_session_grid(dnn_hip_session *s, int *grid) {
     if (!s || !grid) return fail(DNN_HIP_EINVAL, "NULL argument");
-    *grid = s->grid;
+    *grid = s->groups.empty() ? s->grid : s->groups[0]->grid;
     return DNN_HIP_OK;
 }
 
 int dnn_hip_session_kernel(dnn_hip_session *s, int *which) {
     if (!s || !which) return fail(DNN_HIP_EINVAL, "NULL argument");
-    *which = s->kernel_used;
+    *which = s->groups.empty() ? s->kernel_used : s->groups[0]->kernel_used;
     return DNN_HIP_OK;
 }
 
@@ -380,13 +412,95 @@ int dnn_hip_session_last_ms(dnn_hip_session *s, float *ms) {
     return DNN_HIP_OK;
 }
 
+namespace {
+
+// A session of more than MAXB rows: each group of rows decodes in turn, its
+// columns of feed / ids / logits gathered and scattered.  With eos >= 0 a
+// group that stops early is run on (greedy, no stop) to the step where the
+// last group stopped, so every row advances the same number of steps, as in
+// one launch.
+int decode_groups(dnn_hip_session *s, const int *feed, int n_feed_all, const int *n_feed, int n_steps, int eos,
+                  int *ids, float *logits, int *steps_done) {
+    const int B = s->B, V = s->m->V;
+    int nf_max = 0;
+    for (int b = 0; b < B; b++) nf_max = std::max(nf_max, n_feed ? n_feed[b] : n_feed_all);
+    std::vector<int> gfeed, gnf, gids;
+    std::vector<float> glog;
+    std::vector<int> done(s->groups.size(), 0);
+    float ms = 0.f;
+    int r0 = 0;
+    for (size_t gi = 0; gi < s->groups.size(); gi++) {
+        dnn_hip_session *g = s->groups[gi];
+        const int gb = g->B;
+        gfeed.assign((size_t)std::max(nf_max, 1) * gb, 0);
+        gnf.assign(gb, 0);
+        for (int b = 0; b < gb; b++) {
+            gnf[b] = n_feed ? n_feed[r0 + b] : n_feed_all;
+            for (int t = 0; t < gnf[b] && t < nf_max; t++) gfeed[(size_t)t * gb + b] = feed[(size_t)t * B + r0 + b];
+        }
+        gids.assign((size_t)n_steps * gb, 0);
+        if (logits) glog.assign((size_t)n_steps * gb * V, 0.f);
+        int d = 0;
+        int rc = dnn_hip_decode(g, gfeed.data(), 0, gnf.data(), n_steps, eos, gids.data(), logits ? glog.data() : nullptr, &d);
+        if (rc) return rc;
+        float gms = 0.f;
+        dnn_hip_session_last_ms(g, &gms);
+        ms += gms;
+        done[gi] = d;
+        for (int t = 0; t < d; t++)
+            for (int b = 0; b < gb; b++) {
+                if (ids) ids[(size_t)t * B + r0 + b] = gids[(size_t)t * gb + b];
+                if (logits)
+                    memcpy(logits + ((size_t)t * B + r0 + b) * V, glog.data() + ((size_t)t * gb + b) * V, sizeof(float) * V);
+            }
+        r0 += gb;
+    }
+    const int all_done = *std::max_element(done.begin(), done.end());
+    r0 = 0;
+    for (size_t gi = 0; gi < s->groups.size(); gi++) {
+        dnn_hip_session *g = s->groups[gi];
+        const int gb = g->B, more = all_done - done[gi];
+        if (more > 0) {
+            // feed each row its last id, then run greedily without a stop
+            std::vector<int> last(gb);
+            for (int b = 0; b < gb; b++) last[b] = ids ? ids[(size_t)(done[gi] - 1) * B + r0 + b] : 0;
+            gids.assign((size_t)more * gb, 0);
+            if (logits) glog.assign((size_t)more * gb * V, 0.f);
+            int rc = dnn_hip_decode(g, last.data(), 1, nullptr, more, -1, gids.data(), logits ? glog.data() : nullptr, nullptr);
+            if (rc) return rc;
+            float gms = 0.f;
+            dnn_hip_session_last_ms(g, &gms);
+            ms += gms;
+            for (int t = 0; t < more; t++)
+                for (int b = 0; b < gb; b++) {
+                    if (ids) ids[(size_t)(done[gi] + t) * B + r0 + b] = gids[(size_t)t * gb + b];
+                    if (logits)
+                        memcpy(logits + ((size_t)(done[gi] + t) * B + r0 + b) * V, glog.data() + ((size_t)t * gb + b) * V,
+                               sizeof(float) * V);
+                }
+        }
+        r0 += gb;
+    }
+    s->last_ms = ms;
+    if (steps_done) *steps_done = all_done;
+    return DNN_HIP_OK;
+}
+
+}  // namespace
+
 int dnn_hip_decode(dnn_hip_session *s, const int *feed, int n_feed_all, const int *n_feed,
                    int n_steps, int eos, int *ids, float *logits, int *steps_done) {
     if (!s || !feed) return fail(DNN_HIP_EINVAL, "NULL argument");
     dnn_hip_model *m = s->m;
     const int B = s->B;
     if (n_steps <= 0) return fail(DNN_HIP_EINVAL, "n_steps %d", n_steps);
-    if (B > MAXB) return fail(DNN_HIP_EINVAL, "batch %d > %d rows per decode launch", B, MAXB);
+    if (!s->groups.empty()) {
+        if (!ids && eos >= 0) return fail(DNN_HIP_EINVAL, "a multi-group session needs ids when eos >= 0");
+        for (int b = 0; b < B; b++)
+            if ((n_feed ? n_feed[b] : n_feed_all) < 1)
+                return fail(DNN_HIP_EINVAL, "row %d: n_feed %d < 1", b, n_feed ? n_feed[b] : n_feed_all);
+        return decode_groups(s, feed, n_feed_all, n_feed, n_steps, eos, ids, logits, steps_done);
+    }
     std::vector<int> nf(B);
     int nf_max = 0;
     for (int b = 0; b < B; b++) {
@@ -412,13 +526,13 @@ int dnn_hip_decode(dnn_hip_session *s, const int *feed, int n_feed_all, const in
     HIP_TRY(hipDeviceGetAttribute(&lds_max, hipDeviceAttributeMaxSharedMemoryPerBlock, m->device));
     int grid = s->grid_cap;
     if (s->grid_req > 0) grid = std::min(grid, s->grid_req);
-    // One or two rows: the lookahead kernel when its schedule fits (every GEMV
-    // round in at most 3 slots of the grid's non-attention workgroups, and its
-    // LDS); otherwise, and for more rows, decode_v3.
+    // decode_v3 by default; the lookahead kernel (one or two rows) on request,
+    // when its schedule fits (every GEMV round in at most 3 slots of the grid's
+    // non-attention workgroups) and its LDS does.
     const void *kern = nullptr;
     size_t shmem = 0;
     const int rounds = (m->D + 6) / 7 + (3 * m->D / 2 + 6) / 7 + (m->D / 2 + 6) / 7 + (m->F + 6) / 7;
-    if (nb <= 2 && s->kernel_pref != 3 && grid > B * m->H && rounds <= 3 * (grid - B * m->H) &&
+    if (nb <= 2 && s->kernel_pref == 4 && grid > B * m->H && rounds <= 3 * (grid - B * m->H) &&
         lds4_bytes(nb, m->ldD, m->ldF, m->L) <= (size_t)lds_max) {
         kern = decode_lookahead_for(nb, dc);
         shmem = lds4_bytes(nb, m->ldD, m->ldF, m->L);

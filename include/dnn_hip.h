@@ -83,7 +83,8 @@ int dnn_hip_model_destroy(dnn_hip_model *m);
 /* A decode session: the per-layer KV caches of `batch` rows in HBM (K stored
  * transposed, [L][B][H][d_k][max_seq]; V as [L][B][H][max_seq][d_k]) plus the
  * exchange arena of the decode kernel.  Every row starts empty.
- * 1 <= batch <= 8. */
+ * 1 <= batch <= 64.  A launch serves at most 8 rows: a larger session holds
+ * groups of at most 8 rows, decoded one after another by dnn_hip_decode. */
 int dnn_hip_session_create(dnn_hip_model *m, int batch, int max_seq,
                            dnn_hip_session **out);
 /* Empties every row (lengths back to 0). */
@@ -121,10 +122,10 @@ int dnn_hip_session_last_ms(dnn_hip_session *s, float *ms);
 int dnn_hip_session_set_grid(dnn_hip_session *s, int n_workgroups);
 /* Workgroups the last dnn_hip_decode launch on this session used. */
 int dnn_hip_session_grid(dnn_hip_session *s, int *n_workgroups);
-/* Which decode kernel the last dnn_hip_decode launch used: 4 = the layer-
- * lookahead kernel (1-2 rows), 3 = the general one (up to 8 rows).  The
- * environment variable DNN_HIP_DECODE_KERNEL=3, read at session creation,
- * forces the general kernel. */
+/* Which decode kernel the last dnn_hip_decode launch used: 3 = the general
+ * one (up to 8 rows, the default), 4 = the layer-lookahead kernel (1-2 rows),
+ * chosen when the environment variable DNN_HIP_DECODE_KERNEL=4 is set at
+ * session creation and its schedule fits the grid. */
 int dnn_hip_session_kernel(dnn_hip_session *s, int *which);
 
 #ifdef __cplusplus

@@ -100,7 +100,7 @@ def test_c2_gpt2_init_tokens(golden):
     assert list(out) == want
 
 
-@pytest.mark.parametrize("B", [2, 5, 8])
+@pytest.mark.parametrize("B", [2, 5, 8, 20])
 def test_batch_rows_match_independent_runs(c1g, B):
     """Each row of a batched decode equals its own B=1 run (rows differ in
     prompt length, so they switch from prompt to greedy at different steps)."""
@@ -121,18 +121,18 @@ def test_batch_rows_match_independent_runs(c1g, B):
 
 @pytest.mark.parametrize("B", [1, 2])
 def test_lookahead_kernel_equals_general_kernel(golden, c2, monkeypatch, B):
-    """One and two rows run the layer-lookahead kernel; its logits must equal
-    the general kernel's bit for bit (same arithmetic, different schedule)."""
+    """The layer-lookahead kernel (one or two rows, on request) must give the
+    general kernel's logits bit for bit (same arithmetic, different schedule)."""
     _, hm = c2
     toks = np.array(golden["c2_tokens"][:48], dtype=np.int32)
     feed = np.stack([toks] * B, axis=1) if B > 1 else toks
-    s4 = A.HipSession(hm, B, 64)
-    ids4, lg4 = s4.decode(feed, 48, want_logits=True)
-    assert s4.kernel() == 4
-    monkeypatch.setenv("DNN_HIP_DECODE_KERNEL", "3")
     s3 = A.HipSession(hm, B, 64)
     ids3, lg3 = s3.decode(feed, 48, want_logits=True)
     assert s3.kernel() == 3
+    monkeypatch.setenv("DNN_HIP_DECODE_KERNEL", "4")
+    s4 = A.HipSession(hm, B, 64)
+    ids4, lg4 = s4.decode(feed, 48, want_logits=True)
+    assert s4.kernel() == 4
     assert np.array_equal(ids4, ids3)
     assert np.array_equal(lg4.view(np.uint32), lg3.view(np.uint32))
 
@@ -165,11 +165,37 @@ def test_session_bounds_are_errors(c1g):
 
 
 def test_large_batch_is_refused(c1g):
-    """Rows per decode launch are capped at 8; a larger batch is an error at
-    session creation, not a silent split."""
+    """Sessions hold at most 64 rows; more is an error at creation."""
     hm = hip_model(c1g)
     with pytest.raises(A.HipError, match="outside"):
-        A.HipSession(hm, 9, 16)
+        A.HipSession(hm, 65, 16)
+
+
+def test_multi_group_eos_keeps_rows_in_step(c1g):
+    """More than 8 rows run as groups of 8.  With an EOS stop, a group that
+    finishes before the others is run on greedily, so every row advances the
+    same number of steps and each row's ids equal its own independent run.
+    Rows 8..11 (the second group) share one prompt and rows 0..7 another; the
+    EOS id is one the second prompt emits early and the first never does."""
+    hm = hip_model(c1g)
+    B, steps = 12, 40
+    rng = np.random.default_rng(7)
+    pa, pb = rng.integers(0, 128, size=(2, 4)).astype(np.int32)
+    ra = c1g.generate(pa, steps - 3, eos=-1)
+    rb = c1g.generate(pb, steps - 3, eos=-1)
+    cands = [j for j in range(4, 20) if ra[j] not in set(ra[4:j]) and ra[j] not in set(rb[4:])]
+    if not cands:
+        pytest.skip("no EOS id separates the two prompts for this seed")
+    j = cands[0]
+    eos = int(ra[j])
+    feed = np.stack([pb] * 8 + [pa] * 4, axis=1)
+    s = A.HipSession(hm, B, 64)
+    ids, _ = s.decode(feed, steps, n_feed=np.full(B, 4, np.int32), eos=eos)
+    assert ids.shape[0] == steps                # the first group never emits eos
+    assert list(s.lengths()) == [steps] * B
+    for b in range(B):
+        ref = rb if b < 8 else ra
+        assert list(ids[3:, b]) == list(ref[4:steps + 1]), "row %d" % b
 
 
 @pytest.mark.parametrize("init,seed,pseed,key", [("synthetic", 1, 101, "c1"), ("gpt2", 11, 111, "c1g")])
