@@ -34,6 +34,7 @@ CONFIGS = {
     "c2b8": (8192, 768, 12, 12, 2048, 32, 8),
 }
 SEED = {"c1": 1, "c2": 2, "c3": 3, "c2b8": 2}
+KERNELS = {3: "decode_v3<NB,DC>", 4: "decode_v4<NB,DC>", 5: "decode_v5<NB,DC>"}
 
 
 class Ctx(C.Structure):
@@ -205,7 +206,7 @@ def main():
         "device_ms_per_step": round(dev_ms / args.steps, 5),
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": 8000.0, "unit": "GB/s",
                      "frac": round(achieved / 8000.0, 4), "traffic": None,
-                     "kernel": "dnnhip::decode_v3<NB,DC> (one persistent launch = %d steps)" % args.steps,
+                     "kernel": "dnnhip::%s (one persistent launch = %d steps)" % (KERNELS.get(s.kernel(), "?"), args.steps),
                      "algorithmic_bytes_per_launch": nbytes},
     }
     traffic = measured_traffic(args.config, positions)

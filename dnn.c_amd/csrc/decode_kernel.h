@@ -107,7 +107,82 @@ inline size_t lds4_bytes(int nb, int ldD, int ldF, int L) {
            (size_t)4 * (2 * L + 1) + sizeof(LayerOff) * (size_t)L;
 }
 
+// ---- the streaming kernel (one or two rows) --------------------------------
+// Workgroups 0 .. NG-1 run the GEMV phases (7 compute wavefronts + 1 stager),
+// the last B*H*NS run attention, NS workgroups per (row, head), each over
+// every NS-th 32-key chunk.
+constexpr int S_NCW = WPB - 1;    // compute wavefronts per GEMV workgroup
+constexpr int S_SLOT = 1024;      // weight ring slot: one dwordx4 LDS DMA (64 lanes x 16 B)
+constexpr int S_BSLOT = 256;      // bias slot: one dword LDS DMA
+constexpr int S_NBIAS = 8;        // bias slots per compute wavefront
+constexpr int S_MAXREC = 64;      // attention partial records per layer (rows * heads * splits)
+inline int stream_splits(int nb) { return nb == 1 ? 4 : 2; }
+
+// Exchange arena of the streaming kernel (tagged pairs), per layer:
+//   QKV [B][3D] (after bias and RoPE), X1 [B][D], ACT [B][F], X2 [B][D],
+//   AO [B*H*NS][64] unnormalised attention partials (sum_j e^(s_j - m) v_j),
+//   AML [B*H*NS][2] their (m, sum_j e^(s_j - m));
+// then AMAX [2][B][NG][2] (value, index) lm_head argmax partials, double
+// buffered by step parity.
+struct Exch5 {
+    int D, F, B, H, NS, NG;
+    __host__ __device__ size_t nrec() const { return (size_t)B * H * NS; }
+    __host__ __device__ size_t per_layer() const { return (size_t)B * (5 * (size_t)D + F) + nrec() * 66; }
+    __host__ __device__ size_t qkv(int l, int b) const { return per_layer() * l + (size_t)b * 3 * D; }
+    __host__ __device__ size_t x1(int l, int b) const { return per_layer() * l + (size_t)B * 3 * D + (size_t)b * D; }
+    __host__ __device__ size_t act(int l, int b) const { return per_layer() * l + (size_t)B * 4 * D + (size_t)b * F; }
+    __host__ __device__ size_t x2(int l, int b) const {
+        return per_layer() * l + (size_t)B * (4 * (size_t)D + F) + (size_t)b * D;
+    }
+    __host__ __device__ size_t ao(int l) const { return per_layer() * l + (size_t)B * (5 * (size_t)D + F); }
+    __host__ __device__ size_t aml(int l) const { return ao(l) + nrec() * 64; }
+    __host__ __device__ size_t amax(int L, int par, int b, int g) const {
+        return per_layer() * L + (((size_t)par * B + b) * NG + g) * 2;
+    }
+    __host__ __device__ size_t total(int L) const { return per_layer() * L + (size_t)2 * B * NG * 2; }
+};
+
+// LDS of the streaming kernel, byte offsets.  head: ints tok[8] pos[8] done[8]
+// misc[8] and the phase table [5][8]; then the RoPE entries of this step
+// [nb][64], the layer table, attention merge partials [WPB][DK+2], the
+// per-wavefront argmax [S_NCW][MAXB][2], the output blocks [2][sout], the
+// staged rows XS, YS, AS, X1S [nb][ldD] and ACTS [nb][ldF], the weight rings
+// [S_NCW][rs] slots and the bias slots [S_NCW][S_NBIAS].
+struct Lds5 {
+    int rope, lt, part, best, out, xs, ys, as, x1s, acts, ring, bias, total;
+    int rs, sout;
+};
+inline __host__ __device__ Lds5 lds5_layout(int nb, int ldD, int ldF, int L, int sout, int rs) {
+    Lds5 o{};
+    int p = 4 * (32 + 40);
+    auto take = [&](int bytes) { int r = p; p += (bytes + 15) / 16 * 16; return r; };
+    o.rope = take(4 * nb * 64);
+    o.lt = take((int)sizeof(LayerOff) * L);
+    o.part = take(4 * WPB * (DK + 2));
+    o.best = take(4 * S_NCW * MAXB * 2);
+    o.out = take(4 * 2 * sout);
+    o.xs = take(4 * nb * ldD);
+    o.ys = take(4 * nb * ldD);
+    o.as = take(4 * nb * ldD);
+    o.x1s = take(4 * nb * ldD);
+    o.acts = take(4 * nb * ldF);
+    o.bias = take(S_NCW * S_NBIAS * S_BSLOT);
+    o.ring = take(S_NCW * rs * S_SLOT);
+    o.total = p;
+    o.rs = rs;
+    o.sout = sout;
+    return o;
+}
+
+struct StreamArgs {
+    DecodeArgs a;
+    Exch5 ex;
+    Lds5 lds;
+    int ng;                 // GEMV workgroups; the rest of the grid runs attention
+};
+
 const void *decode_kernel_for(int nb, int dc);
 const void *decode_lookahead_for(int nb, int dc);
+const void *decode_stream_for(int nb, int dc);
 
 }  // namespace dnnhip

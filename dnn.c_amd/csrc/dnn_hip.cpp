@@ -68,8 +68,9 @@ struct dnn_hip_session {
     size_t logits_cap = 0;
     int grid_req = 0, grid = 0, grid_cap = 0;
     unsigned next_tag = 1;                    // tags only grow: stale values never match
-    int kernel_pref = 0;                      // 4: the lookahead kernel where it applies
-    int kernel_used = 0;                      // 3 or 4: the kernel of the last launch
+    int kernel_pref = 0;                      // env DNN_HIP_DECODE_KERNEL: 4 / 5: the lookahead / streaming kernel where it applies
+    int kernel_used = 0;                      // 3, 4 or 5: the kernel of the last launch
+    size_t xa_pairs = 0;
     float last_ms = 0.f;
     std::vector<int> h_pos;
     // more than MAXB rows: consecutive groups of at most MAXB rows, each its own
@@ -178,6 +179,37 @@ int grow(T **p, size_t *cap, size_t count) {
 }
 
 int pick_nb(int B) { return B > 4 ? 8 : B > 2 ? 4 : B > 1 ? 2 : 1; }
+
+// The streaming kernel's launch shape for this model, batch and grid, or
+// false where it does not apply (the general kernel runs instead): every GEMV
+// workgroup must own out_proj and down rows (so each takes part in every
+// layer), each compute wavefront's biases of a phase must fit one 64-lane
+// gather, the attention partials one 64-lane merge, and the weight ring must
+// hold the largest unit.
+bool stream_plan(const dnn_hip_model *m, int B, int grid, int lds_max, StreamArgs *sa) {
+    if (B > 2) return false;
+    const int nb = B, NS = stream_splits(nb), NA = B * m->H * NS, NG = grid - NA;
+    if (NG < 1 || NG > m->D || NA > S_MAXREC) return false;
+    const int DC = m->ldD / LDALIGN, FC = m->ldF / LDALIGN;
+    const int nu[5] = {3 * m->D / 2, m->D, m->F, m->D, m->V};
+    const int R[5] = {2, 1, 2, 1, 1};
+    const int out_per_unit[4] = {2, 1, 1, 1};
+    int sout = 0;
+    for (int k = 0; k < 5; k++) {
+        const int n_wg = (nu[k] + NG - 1) / NG;
+        if ((n_wg + S_NCW - 1) / S_NCW * R[k] > WAVE) return false;
+        if (k < 4) sout = std::max(sout, nb * n_wg * out_per_unit[k]);
+    }
+    const int fixed = lds5_layout(nb, m->ldD, m->ldF, m->L, sout, 0).total;
+    int rs = (lds_max - fixed) / (S_NCW * S_SLOT);
+    rs = std::min(rs, 48);
+    if (rs < std::max(2 * DC, FC)) return false;
+    sa->lds = lds5_layout(nb, m->ldD, m->ldF, m->L, sout, rs);
+    if (sa->lds.total > lds_max) return false;
+    sa->ex = Exch5{m->D, m->F, B, m->H, NS, NG};
+    sa->ng = NG;
+    return true;
+}
 
 }  // namespace
 
@@ -314,7 +346,14 @@ int dnn_hip_session_create(dnn_hip_model *m, int B, int max_seq, dnn_hip_session
     // + CH*DK floats of zeroed padding: attention reads whole 32-key chunks,
     // and the rows past max_seq of the last head must stay inside the allocation
     const size_t kv = (size_t)m->L * B * m->H * max_seq * DK + (size_t)CH * DK;
-    const size_t xa_pairs = s->ex.total(m->L);
+    size_t xa_pairs = s->ex.total(m->L);
+    if (B <= 2) {
+        // room for the streaming kernel's exchange layout (its grid <= grid_cap)
+        const int nb = pick_nb(B);
+        const Exch5 e5{m->D, m->F, B, m->H, stream_splits(nb), s->grid_cap};
+        xa_pairs = std::max(xa_pairs, e5.total(m->L));
+    }
+    s->xa_pairs = xa_pairs;
     if (kv * sizeof(float) >= 0x7fffffffu || xa_pairs * 8 >= 0x7fffffffu) {
         delete s;
         return fail(DNN_HIP_EINVAL, "KV cache of %zu bytes per tensor / exchange of %zu bytes: each must stay < 2 GiB",
@@ -531,8 +570,16 @@ int dnn_hip_decode(dnn_hip_session *s, const int *feed, int n_feed_all, const in
     // non-attention workgroups) and its LDS does.
     const void *kern = nullptr;
     size_t shmem = 0;
+    StreamArgs sa{};
+    bool stream = false;
+    if (s->kernel_pref == 5 && stream_plan(m, B, grid, lds_max, &sa) &&
+        sa.ex.total(m->L) <= s->xa_pairs) {
+        kern = decode_stream_for(nb, dc);
+        shmem = (size_t)sa.lds.total;
+        stream = kern != nullptr;
+    }
     const int rounds = (m->D + 6) / 7 + (3 * m->D / 2 + 6) / 7 + (m->D / 2 + 6) / 7 + (m->F + 6) / 7;
-    if (nb <= 2 && s->kernel_pref == 4 && grid > B * m->H && rounds <= 3 * (grid - B * m->H) &&
+    if (!kern && nb <= 2 && s->kernel_pref == 4 && grid > B * m->H && rounds <= 3 * (grid - B * m->H) &&
         lds4_bytes(nb, m->ldD, m->ldF, m->L) <= (size_t)lds_max) {
         kern = decode_lookahead_for(nb, dc);
         shmem = lds4_bytes(nb, m->ldD, m->ldF, m->L);
@@ -542,7 +589,7 @@ int dnn_hip_decode(dnn_hip_session *s, const int *feed, int n_feed_all, const in
         shmem = lds_bytes(nb, m->ldD, m->ldF);
     }
     if (!kern) return fail(DNN_HIP_EINVAL, "d_model %d: the decode kernels cover d_model <= %d", m->D, 3 * LDALIGN);
-    s->kernel_used = kern == decode_kernel_for(nb, dc) ? 3 : 4;
+    s->kernel_used = stream ? 5 : kern == decode_kernel_for(nb, dc) ? 3 : 4;
     int rc = grow(&s->feed, &s->feed_cap, (size_t)nf_max * B);
     if (!rc) rc = grow(&s->ids, &s->ids_cap, (size_t)n_steps * B);
     if (!rc && logits) rc = grow(&s->logits, &s->logits_cap, (size_t)n_steps * B * m->V);
@@ -581,7 +628,8 @@ int dnn_hip_decode(dnn_hip_session *s, const int *feed, int n_feed_all, const in
     a.ids = s->ids; a.logits = logits ? s->logits : nullptr;
     a.n_steps = n_steps; a.eos = eos; a.step0 = s->next_tag; a.err = s->err; a.steps_done = s->steps_done;
     s->next_tag += (unsigned)n_steps;
-    void *kargs[] = {&a};
+    sa.a = a;
+    void *kargs[] = {stream ? static_cast<void *>(&sa) : static_cast<void *>(&a)};
     HIP_TRY(hipEventRecord(s->ev0, s->stream));
     HIP_TRY(hipLaunchKernel(kern, dim3(grid), dim3(BLOCK), kargs, shmem, s->stream));
     HIP_TRY(hipEventRecord(s->ev1, s->stream));

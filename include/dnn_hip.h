@@ -123,9 +123,10 @@ int dnn_hip_session_set_grid(dnn_hip_session *s, int n_workgroups);
 /* Workgroups the last dnn_hip_decode launch on this session used. */
 int dnn_hip_session_grid(dnn_hip_session *s, int *n_workgroups);
 /* Which decode kernel the last dnn_hip_decode launch used: 3 = the general
- * one (up to 8 rows, the default), 4 = the layer-lookahead kernel (1-2 rows),
- * chosen when the environment variable DNN_HIP_DECODE_KERNEL=4 is set at
- * session creation and its schedule fits the grid. */
+ * one (up to 8 rows, the default), 4 = the layer-lookahead kernel, 5 = the
+ * streaming kernel (both 1-2 rows), chosen when the environment variable
+ * DNN_HIP_DECODE_KERNEL is 4 or 5 at session creation and the kernel's
+ * schedule fits the model and grid. */
 int dnn_hip_session_kernel(dnn_hip_session *s, int *which);
 
 #ifdef __cplusplus
