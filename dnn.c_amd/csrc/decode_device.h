@@ -66,6 +66,18 @@ __device__ __forceinline__ float wave_sum(float v) {
     v += dpp<0x143, 0xc>(v, 0.f);     // row_bcast:31 into rows 2, 3
     return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 63));
 }
+// Two independent sums, their DPP steps interleaved (each hides the other's
+// DPP hazard wait states); same order of additions as wave_sum.
+__device__ __forceinline__ void wave_sum2(float &a, float &b) {
+    a += dpp<0xb1, 0xf>(a, 0.f);  b += dpp<0xb1, 0xf>(b, 0.f);
+    a += dpp<0x4e, 0xf>(a, 0.f);  b += dpp<0x4e, 0xf>(b, 0.f);
+    a += dpp<0x141, 0xf>(a, 0.f); b += dpp<0x141, 0xf>(b, 0.f);
+    a += dpp<0x140, 0xf>(a, 0.f); b += dpp<0x140, 0xf>(b, 0.f);
+    a += dpp<0x142, 0xa>(a, 0.f); b += dpp<0x142, 0xa>(b, 0.f);
+    a += dpp<0x143, 0xc>(a, 0.f); b += dpp<0x143, 0xc>(b, 0.f);
+    a = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, a), 63));
+    b = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, b), 63));
+}
 __device__ __forceinline__ float wave_max(float v) {
     v = fmaxf(v, dpp<0xb1, 0xf>(v, -INFINITY));
     v = fmaxf(v, dpp<0x4e, 0xf>(v, -INFINITY));

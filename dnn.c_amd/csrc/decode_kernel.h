@@ -88,6 +88,14 @@ struct DecodeArgs {
     int *steps_done;
 };
 
+// Sessions decoded by one launch of the general kernel (groups of a session
+// of more than MAXB rows): session i on workgroups [i * per, (i + 1) * per).
+constexpr int MAX_GROUPS = MAX_ROWS / MAXB;
+struct MultiArgs {
+    DecodeArgs a[MAX_GROUPS];
+    int n, per;
+};
+
 // Dynamic LDS of the decode kernel (bytes): per-row token / position / done
 // flags, per-wavefront argmax and attention partials, the double-buffered
 // output block of a GEMV round (OUT [2][WPB][2*MAXB]), then the staged rows
@@ -108,13 +116,13 @@ inline size_t lds4_bytes(int nb, int ldD, int ldF, int L) {
 }
 
 // ---- the streaming kernel (one or two rows) --------------------------------
-// Workgroups 0 .. NG-1 run the GEMV phases (7 compute wavefronts + 1 stager),
-// the last B*H*NS run attention, NS workgroups per (row, head), each over
-// every NS-th 32-key chunk.
-constexpr int S_NCW = WPB - 1;    // compute wavefronts per GEMV workgroup
+// Workgroups 0 .. NG-1 run the GEMV phases (wavefront 0 streams weights,
+// wavefronts 1-6 compute, wavefront 7 stages), the last B*H*NS run attention,
+// NS workgroups per (row, head), each over every NS-th 32-key chunk.
+constexpr int S_NCW = WPB - 2;    // compute wavefronts per GEMV workgroup
 constexpr int S_SLOT = 1024;      // weight ring slot: one dwordx4 LDS DMA (64 lanes x 16 B)
-constexpr int S_BSLOT = 256;      // bias slot: one dword LDS DMA
-constexpr int S_NBIAS = 8;        // bias slots per compute wavefront
+constexpr int S_BSLOT = 256;      // bias slot: one dword LDS DMA (a phase's biases)
+constexpr int S_NBIAS = 8;        // phases in flight (bias slots)
 constexpr int S_MAXREC = 64;      // attention partial records per layer (rows * heads * splits)
 inline int stream_splits(int nb) { return nb == 1 ? 4 : 2; }
 
@@ -143,18 +151,21 @@ struct Exch5 {
 };
 
 // LDS of the streaming kernel, byte offsets.  head: ints tok[8] pos[8] done[8]
-// misc[8] and the phase table [5][8]; then the RoPE entries of this step
-// [nb][64], the layer table, attention merge partials [WPB][DK+2], the
-// per-wavefront argmax [S_NCW][MAXB][2], the output blocks [2][sout], the
-// staged rows XS, YS, AS, X1S [nb][ldD] and ACTS [nb][ldF], the weight rings
-// [S_NCW][rs] slots and the bias slots [S_NCW][S_NBIAS].
+// misc[8], the phase table [5][8], the ring slot where each phase in flight
+// starts [S_NBIAS] and its last DMA's issue count [S_NBIAS]; then the RoPE
+// entries of this step [nb][64], the layer table, attention merge partials
+// [WPB][DK+2], the per-wavefront argmax [S_NCW][MAXB][2], the output blocks
+// [2][sout], the staged rows XS, X1S [nb][ldD], then YS, AS [nb][ldD] sharing
+// their space with ACTS [nb][ldF] (the down projection's input is staged after
+// the last read of YS and AS in a layer, and YS is staged again after the
+// down projection), the bias slots [S_NBIAS] and the weight ring [rs] slots.
 struct Lds5 {
     int rope, lt, part, best, out, xs, ys, as, x1s, acts, ring, bias, total;
     int rs, sout;
 };
 inline __host__ __device__ Lds5 lds5_layout(int nb, int ldD, int ldF, int L, int sout, int rs) {
     Lds5 o{};
-    int p = 4 * (32 + 40);
+    int p = 4 * (32 + 40 + 2 * S_NBIAS);
     auto take = [&](int bytes) { int r = p; p += (bytes + 15) / 16 * 16; return r; };
     o.rope = take(4 * nb * 64);
     o.lt = take((int)sizeof(LayerOff) * L);
@@ -162,12 +173,12 @@ inline __host__ __device__ Lds5 lds5_layout(int nb, int ldD, int ldF, int L, int
     o.best = take(4 * S_NCW * MAXB * 2);
     o.out = take(4 * 2 * sout);
     o.xs = take(4 * nb * ldD);
-    o.ys = take(4 * nb * ldD);
-    o.as = take(4 * nb * ldD);
     o.x1s = take(4 * nb * ldD);
-    o.acts = take(4 * nb * ldF);
-    o.bias = take(S_NCW * S_NBIAS * S_BSLOT);
-    o.ring = take(S_NCW * rs * S_SLOT);
+    o.ys = take(4 * nb * (2 * ldD > ldF ? 2 * ldD : ldF));
+    o.as = o.ys + 4 * nb * ldD;
+    o.acts = o.ys;
+    o.bias = take(S_NBIAS * S_BSLOT);
+    o.ring = take(rs * S_SLOT);
     o.total = p;
     o.rs = rs;
     o.sout = sout;
@@ -182,6 +193,7 @@ struct StreamArgs {
 };
 
 const void *decode_kernel_for(int nb, int dc);
+const void *decode_multi_for(int dc);
 const void *decode_lookahead_for(int nb, int dc);
 const void *decode_stream_for(int nb, int dc);
 

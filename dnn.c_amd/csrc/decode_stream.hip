@@ -4,18 +4,19 @@
 // transformer.c:211-416), scheduled so that no weight byte is fetched on the
 // critical path:
 //
-//   * GEMV workgroups (0 .. NG-1): 7 compute wavefronts and 1 stager.  Each
-//     compute wavefront owns a fixed, balanced share of every GEMV phase (QKV,
-//     out_proj, gate/up, down, lm_head) and streams its weight rows into its
-//     own LDS ring with direct-to-LDS DMA (buffer_load ... lds), in the order
-//     it will consume them, as far ahead as the ring allows (about one layer).
-//     Only the compute wavefronts issue DMA, and only DMA: the in-order
-//     completion of vector memory lets each wait for exactly the rows it needs
-//     next (s_waitcnt vmcnt(n)).  The stager issues every poll of the exchange
-//     arena, so a poll never queues behind a weight fetch; it stages the phase
-//     input into LDS (with the RMSNorm applied where the phase has one), meets
-//     the compute wavefronts at a workgroup barrier, and after a second one
-//     writes the workgroup's outputs as one coalesced block of tagged pairs.
+//   * GEMV workgroups (0 .. NG-1) own a balanced, contiguous share of every
+//     GEMV phase (QKV, out_proj, gate/up, down, lm_head).  Wavefront 0 streams
+//     the workgroup's weight rows, in the order they will be consumed and
+//     about one layer ahead, into one LDS ring with direct-to-LDS DMA
+//     (buffer_load ... lds); it issues nothing else, so the in-order
+//     completion of vector memory lets it wait for exactly the phase the
+//     workgroup needs next (s_waitcnt vmcnt(n)).  Wavefront 7, the stager,
+//     issues every poll of the exchange arena, so a poll never queues behind a
+//     weight fetch; it stages the phase input into LDS (with the RMSNorm
+//     applied where the phase has one).  All eight meet at a workgroup barrier,
+//     wavefronts 1-6 compute the phase's dot products from the ring, and after
+//     a second barrier the stager writes the workgroup's outputs as one
+//     coalesced block of tagged pairs.
 //   * attention workgroups (the last B*H*NS): NS per (row, head); split s takes
 //     the 32-key chunks c = s (mod NS), wavefront w the chunks with
 //     c / NS = w (mod 8).  The cached keys and values of a chunk are loaded
@@ -32,16 +33,15 @@ namespace dnnhip {
 
 namespace {
 
-constexpr int NCW = S_NCW;
 constexpr int NPH = 5;              // phase kinds: A (qkv), C (out), D (gate/up), E (down), F (lm_head)
 enum { K_A = 0, K_C = 1, K_D = 2, K_E = 3, K_F = 4 };
 
-// LDS head (ints): tok[8] pos[8] done[8] misc[8], then the phase table
-// ph[kind][8] = {nu, R, chunks, u0, n, pre, -, -}: units of the phase, rows per
-// unit, 256-float chunks per row, this workgroup's first unit and unit count,
-// and the units of the layer's earlier phases in this workgroup.
-enum { H_TOK = 0, H_POS = 8, H_DONE = 16, H_STOP = 24, H_LSUM = 25, H_PH = 32 };
-enum { P_NU = 0, P_R = 1, P_CH = 2, P_U0 = 3, P_N = 4, P_PRE = 5 };
+// LDS head (ints): tok[8] pos[8] done[8] misc[8], the phase table
+// ph[kind][8] = {nu, R, chunks, u0, n, -, -, -} (units of the phase, rows per
+// unit, 256-float chunks per row, this workgroup's first unit and unit count),
+// then PST / PEND [S_NBIAS] of the weight stream.
+enum { H_TOK = 0, H_POS = 8, H_DONE = 16, H_STOP = 24, H_PH = 32, H_PST = 72, H_PEND = 72 + S_NBIAS };
+enum { P_NU = 0, P_R = 1, P_CH = 2, P_U0 = 3, P_N = 4 };
 
 __device__ __forceinline__ int ufl(int v) { return __builtin_amdgcn_readfirstlane(v); }
 
@@ -52,9 +52,9 @@ __device__ __forceinline__ unsigned lds_addr(const void *p) {
 // One direct-to-LDS DMA: 64 lanes x 16 bytes from rsrc + voff (per lane) to
 // LDS [m0 + 16 * lane].  Non-temporal: weights are read once per step.  M0 is
 // written here only; nothing else in these kernels uses it.
-__device__ __forceinline__ void dma16(rsrc_t r, unsigned lds, unsigned voff) {
-    asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tbuffer_load_dwordx4 %1, %2, 0 offen nt lds"
-                 :: "s"(lds), "v"(voff), "s"(r) : "memory", "m0");
+__device__ __forceinline__ void dma16(rsrc_t r, unsigned lds, unsigned voff, unsigned soff) {
+    asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tbuffer_load_dwordx4 %1, %2, %3 offen nt lds"
+                 :: "s"(lds), "v"(voff), "s"(r), "s"(soff) : "memory", "m0");
 }
 // 64 lanes x 4 bytes (a gather: voff per lane) to LDS [m0 + 4 * lane].
 __device__ __forceinline__ void dma4(rsrc_t r, unsigned lds, unsigned voff) {
@@ -94,121 +94,95 @@ __device__ __forceinline__ LayerOff lds_layer(const LayerOff *lt, int l) {
 }
 
 // ---------------------------------------------------------------------------
-// A compute wavefront's weight stream.  Stream order per step: for each layer
-// the wavefront's units of A, C, D, E, then of F; each phase in which it owns
-// units starts with one bias item (a dword gather of its units' biases into
-// a bias slot), then one item per unit (R rows x ch chunks of 256 floats, one
-// ring slot per chunk).  Unit j of a workgroup's phase (j = 0 .. n-1, the
-// workgroup owning units u0 .. u0+n-1) belongs to compute wavefront
-// (j + rot) mod 7, rot counting the workgroup's earlier units of the step, so
-// every wavefront streams about the same bytes per layer.
-struct Stream {
-    int w, rs;
-    unsigned ring, bias;            // LDS byte addresses of this wavefront's ring / bias slots
-    // issue cursor
-    int it, il, ik, ii, im;         // step, layer, kind, next unit (-1: bias item), units of this wavefront
-    int tail, btail, issued;        // ring slots / bias slots / DMA instructions issued
-    // consume cursor
-    int head, bhead, done;          // ring slots / bias slots / DMA instructions consumed
+// The workgroup's weight stream (wavefront 0).  Stream order per step: for
+// each layer the workgroup's units of A, C, D, E, then of F.  Each phase
+// starts with one bias item (a 64-lane dword gather of the phase's biases into
+// a bias slot; gate/up: gate biases in lanes 0-31, up in 32-63), then one item
+// per unit: R rows x ch chunks of 256 floats, one ring slot per chunk, units
+// in order.  A phase is admitted when fewer than S_NBIAS phases are in flight;
+// a unit when the ring has room for it.
+struct Issuer {
+    int rs;
+    unsigned ring, bias;            // LDS byte addresses of the ring / bias slots
+    unsigned vl;                    // 16 * lane: the per-lane byte offset of a slot DMA
+    int it, il, ik, ij;             // next item: step, layer, kind, unit (-1: bias item)
+    int n, R, ch;                   // the current phase: units, rows per unit, chunks per row
+    uint32_t row;                   // byte offset of the next unit's first row
+    uint32_t ld;                    // byte distance of a unit's rows
+    int slot;                       // tail % rs
+    int tail, head;                 // ring slots issued / released
+    int btail, bhead;               // phases issued / released
+    int issued;                     // DMA instructions issued
 };
 
-struct PhaseOf {                    // this wavefront's units of one phase
-    int nu, R, ch, u0, n, j0, m;
+struct PhaseOf {                    // this workgroup's units of one phase
+    int R, ch, u0, n;
 };
 
-__device__ __forceinline__ PhaseOf phase_of(const int *ph, int w, int l, int k, int lsum) {
+__device__ __forceinline__ PhaseOf phase_of(const int *ph, int k) {
     PhaseOf p;
     const int *e = ph + 8 * k;
-    p.nu = ufl(e[P_NU]); p.R = ufl(e[P_R]); p.ch = ufl(e[P_CH]);
-    p.u0 = ufl(e[P_U0]); p.n = ufl(e[P_N]);
-    const int rot = ufl((l * lsum + e[P_PRE]) % NCW);
-    p.j0 = ufl((w - rot + NCW) % NCW);
-    p.m = p.n > p.j0 ? ufl((p.n - 1 - p.j0) / NCW + 1) : 0;
+    p.R = ufl(e[P_R]); p.ch = ufl(e[P_CH]); p.u0 = ufl(e[P_U0]); p.n = ufl(e[P_N]);
     return p;
 }
 
-// float offsets of row r of unit u, and of its bias
-__device__ __forceinline__ uint32_t row_off(const DecodeArgs &a, const LayerOff &w, int k, int u, int r) {
-    switch (k) {
-        case K_A: return w.wqkv + (uint32_t)(2 * u + r) * a.ldD;
-        case K_C: return w.wo + (uint32_t)u * a.ldD;
-        case K_D: return w.wgu + (uint32_t)(2 * u + r) * a.ldD;
-        case K_E: return w.wd + (uint32_t)u * a.ldF;
-        default: return a.embed + (uint32_t)u * a.ldD;
-    }
-}
-__device__ __forceinline__ uint32_t bias_off(const DecodeArgs &a, const LayerOff &w, int k, int u, int r) {
-    switch (k) {
-        case K_A: return w.bqkv + (uint32_t)(2 * u + r);
-        case K_C: return w.bo + (uint32_t)u;
-        case K_D: return (r == 0 ? w.bg : w.bu) + (uint32_t)u;
-        case K_E: return w.bd + (uint32_t)u;
-        default: return a.lm_bias + (uint32_t)u;
-    }
-}
-
-// advance the issue cursor to the next phase in which this wavefront owns units
-__device__ __forceinline__ void next_phase(Stream &st, const int *ph, int L, int lsum, int n_steps) {
-    for (;;) {
-        if (st.ik == K_F) { st.ik = K_A; st.il = 0; st.it++; }
-        else if (st.ik == K_E) { if (st.il == L - 1) st.ik = K_F; else { st.ik = K_A; st.il++; } }
-        else st.ik++;
-        if (st.it >= n_steps) { st.im = 0; return; }
-        const PhaseOf p = phase_of(ph, st.w, st.ik == K_F ? L : st.il, st.ik, lsum);
-        if (p.m > 0) { st.im = p.m; st.ii = -1; return; }
-    }
-}
-
-// Issue stream items while they fit: ring slots free, fewer than S_NBIAS
-// phases in flight.
-__device__ __forceinline__ void top_up(Stream &st, const DecodeArgs &a, const LayerOff *lt, const int *ph, int lsum,
-                                       rsrc_t rw, int lane) {
-    while (st.it < a.n_steps) {
-        const int lph = st.ik == K_F ? a.L : st.il;
-        const PhaseOf p = phase_of(ph, st.w, lph, st.ik, lsum);
-        const LayerOff w = lds_layer(lt, st.ik == K_F ? 0 : st.il);
-        if (st.ii < 0) {
-            if (st.btail - st.bhead >= S_NBIAS) return;
-            // lane = i * R + r: bias r of the wavefront's i-th unit (lanes past
-            // the last unit repeat unit 0)
-            const int i = lane / p.R, r = lane - i * p.R;
-            const int u = p.u0 + p.j0 + NCW * (i < p.m ? i : 0);
-            dma4(rw, st.bias + (unsigned)((st.btail % S_NBIAS) * S_BSLOT), bias_off(a, w, st.ik, u, r) * 4u);
-            st.btail++;
-            st.issued++;
-            st.ii = 0;
-            continue;
-        }
-        const int slots = p.R * p.ch;
-        if (st.tail + slots - st.head > st.rs) return;
-        const int u = p.u0 + p.j0 + NCW * st.ii;
-        int slot = st.tail % st.rs;
-        for (int r = 0; r < p.R; r++) {
-            const uint32_t ro = row_off(a, w, st.ik, u, r);
-            for (int c = 0; c < p.ch; c++) {
-                dma16(rw, st.ring + (unsigned)(slot * S_SLOT), (ro + (uint32_t)c * 256) * 4u + (unsigned)lane * 16u);
-                slot = slot + 1 == st.rs ? 0 : slot + 1;
+// Issue up to `budget` DMA instructions of the stream, as far as they fit.
+// s_pst / s_pend [S_NBIAS]: ring slot where each phase in flight starts, and
+// the issue count after its last DMA.
+__device__ __forceinline__ void top_up(Issuer &q, int budget, const DecodeArgs &a, const LayerOff *lt, const int *ph,
+                                       int *s_pst, int *s_pend, rsrc_t rw, int lane) {
+    while (q.it < a.n_steps && budget > 0) {
+        if (q.ij < 0) {
+            // phase start: its parameters, then the bias gather
+            if (q.btail - q.bhead >= S_NBIAS) return;
+            const PhaseOf p = phase_of(ph, q.ik);
+            q.n = p.n; q.R = p.R; q.ch = p.ch;
+            const LayerOff *w = lt + (q.ik == K_F ? 0 : q.il);
+            uint32_t rbase, ld, bbase;
+            int i = lane;
+            switch (q.ik) {
+                case K_A: rbase = w->wqkv + 2u * p.u0 * a.ldD; ld = a.ldD; bbase = w->bqkv + 2u * p.u0;
+                          if (i >= 2 * p.n) i = 0; break;
+                case K_C: rbase = w->wo + (uint32_t)p.u0 * a.ldD; ld = a.ldD; bbase = w->bo + p.u0;
+                          if (i >= p.n) i = 0; break;
+                case K_D: rbase = w->wgu + 2u * p.u0 * a.ldD; ld = a.ldD;
+                          if ((i & 31) >= p.n) i = 0;
+                          bbase = (i < 32 ? w->bg : w->bu - 32u) + p.u0; break;
+                case K_E: rbase = w->wd + (uint32_t)p.u0 * a.ldF; ld = a.ldF; bbase = w->bd + p.u0;
+                          if (i >= p.n) i = 0; break;
+                default:  rbase = a.embed + (uint32_t)p.u0 * a.ldD; ld = a.ldD; bbase = a.lm_bias + p.u0;
+                          if (i >= p.n) i = 0; break;
             }
+            q.row = (uint32_t)ufl((int)rbase) * 4u;
+            q.ld = (uint32_t)ufl((int)ld) * 4u;
+            dma4(rw, q.bias + (unsigned)((q.btail % S_NBIAS) * S_BSLOT), (bbase + (uint32_t)i) * 4u);
+            if (lane == 0) s_pst[q.btail % S_NBIAS] = q.slot;
+            q.issued++;
+            budget--;
+            q.ij = 0;
+        } else {
+            const int slots = q.R * q.ch;
+            if (q.tail + slots - q.head > q.rs) return;
+            for (int r = 0; r < q.R; r++)
+                for (int c = 0; c < q.ch; c++) {
+                    dma16(rw, q.ring + (unsigned)(q.slot * S_SLOT), q.vl, q.row + (uint32_t)r * q.ld + (uint32_t)c * 1024u);
+                    q.slot = q.slot + 1 == q.rs ? 0 : q.slot + 1;
+                }
+            q.row += (uint32_t)q.R * q.ld;
+            q.tail += slots;
+            q.issued += slots;
+            budget -= slots;
+            q.ij++;
         }
-        st.tail += slots;
-        st.issued += slots;
-        if (++st.ii == st.im) next_phase(st, ph, a.L, lsum, a.n_steps);
+        if (q.ij == q.n) {                      // phase complete (possibly empty): record it, go to the next
+            if (lane == 0) s_pend[q.btail % S_NBIAS] = q.issued;
+            q.btail++;
+            q.ij = -1;
+            if (q.ik == K_F) { q.ik = K_A; q.il = 0; q.it++; }
+            else if (q.ik == K_E) { if (q.il == a.L - 1) q.ik = K_F; else { q.ik = K_A; q.il++; } }
+            else q.ik++;
+        }
     }
-}
-
-// The next unit of the consume cursor (slots slots): issue it if the ring had
-// no room for it yet (the units before it are consumed, so it fits now), wait
-// for its DMA, return its first ring slot.
-__device__ __forceinline__ int unit_ready(Stream &st, const DecodeArgs &a, const LayerOff *lt, const int *ph, int lsum,
-                                          rsrc_t rw, int lane, int slots) {
-    const int need = st.done + slots;
-    for (int guard = 0; st.issued < need && guard < 4; guard++) top_up(st, a, lt, ph, lsum, rw, lane);
-    if (st.issued < need) {                  // cannot happen: the ring holds any one unit
-        atomicOr(a.err, 2);
-        return 0;
-    }
-    wait_vm(st.issued - need);
-    return st.head % st.rs;
 }
 
 // ---------------------------------------------------------------------------
@@ -434,21 +408,16 @@ decode_v5(StreamArgs sa) {
     for (int i = tid; i < 32; i += BLOCK) hd[i] = (i >= H_POS && i < H_POS + NB) ? a.pos[i - H_POS] : 0;
     for (int i = tid; i < L * (int)(sizeof(LayerOff) / 4); i += BLOCK)
         reinterpret_cast<uint32_t *>(s_lt)[i] = reinterpret_cast<const uint32_t *>(a.layers)[i];
-    for (int i = tid; i < NB * (4 * ldD + ldF); i += BLOCK) xs[i] = 0.f;   // XS, YS, AS, X1S, ACTS are adjacent
+    for (int i = tid; i < NB * (2 * ldD + (2 * ldD > ldF ? 2 * ldD : ldF)); i += BLOCK)
+        xs[i] = 0.f;                                         // XS, X1S, YS / AS / ACTS are adjacent
     if (tid < NPH) {
         const int k = tid;
         const int nu = k == K_A ? 3 * D / 2 : k == K_C ? D : k == K_D ? F : k == K_E ? D : V;
         const int R = (k == K_A || k == K_D) ? 2 : 1;
         const int ch = k == K_E ? ldF / 256 : ldD / 256;
         const int u0 = (int)((long)nu * g0 / NG), u1 = (int)((long)nu * (g0 + 1) / NG);
-        int pre = 0;
-        for (int kk = 0; kk < k && kk < K_F; kk++) {
-            const int nk = kk == K_A ? 3 * D / 2 : kk == K_C ? D : kk == K_D ? F : D;
-            pre += (int)((long)nk * (g0 + 1) / NG) - (int)((long)nk * g0 / NG);
-        }
         int *e = s_ph + 8 * k;
-        e[P_NU] = nu; e[P_R] = R; e[P_CH] = ch; e[P_U0] = u0; e[P_N] = u1 - u0; e[P_PRE] = k == K_F ? 0 : pre;
-        if (k == K_F) hd[H_LSUM] = pre;      // units of A, C, D, E in this workgroup
+        e[P_NU] = nu; e[P_R] = R; e[P_CH] = ch; e[P_U0] = u0; e[P_N] = u1 - u0;
     }
     __syncthreads();
 
@@ -486,18 +455,34 @@ decode_v5(StreamArgs sa) {
                         const float tv = ld1s<CP_SC1>(rv, vvo, (unsigned)(jj * DK * 4));
                         vr[jj] = j0 + jj < p ? tv : 0.f;
                     }
-                    if (!have_q) { q = poll1(xa, (long)(ex.qkv(l, b) + h * DK + lane), tag, wt); have_q = true; }
-                    asm volatile("" : "+v"(q));
                     const bool has_new = p >= j0 && p < j0 + CH;
                     float kn = 0.f, vn = 0.f;
+                    {
+                        // this step's q (first chunk) and new k, v (the chunk holding
+                        // position p), polled together
+                        const size_t qp = ex.qkv(l, b) + h * DK + lane;
+                        const bool wq = !have_q;
+                        wt.reset();
+                        for (;;) {
+                            u2 v0 = {0u, tag}, v1 = {0u, tag}, v2 = {0u, tag};
+                            if (wq) v0 = __builtin_amdgcn_raw_buffer_load_b64(xa, (unsigned)(qp * 8), 0, CP_SC1);
+                            if (has_new) {
+                                v1 = __builtin_amdgcn_raw_buffer_load_b64(xa, (unsigned)((qp + D) * 8), 0, CP_SC1);
+                                v2 = __builtin_amdgcn_raw_buffer_load_b64(xa, (unsigned)((qp + 2 * D) * 8), 0, CP_SC1);
+                            }
+                            if (wq) q = as_float(v0.x);
+                            kn = as_float(v1.x);
+                            vn = as_float(v2.x);
+                            if (__all(v0.y == tag && v1.y == tag && v2.y == tag) || !wt.again()) break;
+                        }
+                        have_q = true;
+                    }
+                    asm volatile("" : "+v"(q));
                     if (has_new) {
-                        kn = poll1(xa, (long)(ex.qkv(l, b) + D + h * DK + lane), tag, wt);
-                        vn = poll1(xa, (long)(ex.qkv(l, b) + 2 * D + h * DK + lane), tag, wt);
-                        // append position p (transformer.c:76-93) and wait until the
-                        // stores are complete: later steps read them back
+                        // append position p (transformer.c:76-93); the stores are
+                        // waited for at the end of the layer (later steps read them)
                         st1(rk, (head + (size_t)lane * a.max_seq + p) * 4, kn);
                         st1(rv, (head + (size_t)p * DK + lane) * 4, vn);
-                        __builtin_amdgcn_s_waitcnt(0x0f70);                   // vmcnt(0)
                     }
                     float s = 0.f;
 #pragma unroll
@@ -541,6 +526,7 @@ decode_v5(StreamArgs sa) {
                     put(xa, ex.ao(l) + (size_t)rec * DK + lane, O, tag);
                     if (lane < 2) put(xa, ex.aml(l) + (size_t)rec * 2 + lane, lane == 0 ? M : Ls, tag);
                 }
+                __builtin_amdgcn_s_waitcnt(0x0f70);                           // vmcnt(0): cache appends done
                 __syncthreads();
             }
             if (a.eos >= 0) {
@@ -565,8 +551,7 @@ decode_v5(StreamArgs sa) {
         return;
     }
 
-    const int lsum = hd[H_LSUM];
-    if (wid == NCW) {
+    if (wid == WPB - 1) {
         // ================= stager =================
         int tok[NB];
         int t = 0;
@@ -667,7 +652,7 @@ decode_v5(StreamArgs sa) {
             if (lane < NB) {
                 float v = -INFINITY;
                 int i = 0x7fffffff;
-                for (int ww = 0; ww < NCW; ww++) {
+                for (int ww = 0; ww < S_NCW; ww++) {
                     const float vv = s_best[(ww * MAXB + lane) * 2];
                     const int ii = __builtin_bit_cast(int, s_best[(ww * MAXB + lane) * 2 + 1]);
                     if (vv > v || (vv == v && ii < i)) { v = vv; i = ii; }
@@ -698,169 +683,193 @@ decode_v5(StreamArgs sa) {
         return;
     }
 
-    // ================= compute wavefront =================
-    Stream st;
-    st.w = wid;
-    st.rs = lo.rs;
-    st.ring = lds_addr(lds + lo.ring) + (unsigned)(wid * lo.rs * S_SLOT);
-    st.bias = lds_addr(lds + lo.bias) + (unsigned)(wid * S_NBIAS * S_BSLOT);
-    st.it = 0; st.il = 0; st.ik = K_A; st.ii = -1; st.im = 0;
-    st.tail = st.btail = st.issued = 0;
-    st.head = st.bhead = st.done = 0;
-    {
-        const PhaseOf p = phase_of(s_ph, wid, 0, K_A, lsum);
-        if (p.m > 0) st.im = p.m; else next_phase(st, s_ph, L, lsum, a.n_steps);
+    int *s_pst = hd + H_PST, *s_pend = hd + H_PEND;
+    const float *ring = reinterpret_cast<const float *>(lds + lo.ring);
+    const float *bslot = reinterpret_cast<const float *>(lds + lo.bias);
+    if (wid == 0) {
+        // ================= weight stream =================
+        Issuer q;
+        q.rs = lo.rs;
+        q.ring = lds_addr(lds + lo.ring);
+        q.bias = lds_addr(lds + lo.bias);
+        q.vl = 16u * (unsigned)lane;
+        q.it = 0; q.il = 0; q.ik = K_A; q.ij = -1;
+        q.n = q.R = q.ch = 0; q.row = q.ld = 0;
+        q.slot = q.tail = q.head = q.btail = q.bhead = q.issued = 0;
+        top_up(q, 1 << 20, a, s_lt, s_ph, s_pst, s_pend, rw, lane);     // fill the ring
+        int t = 0;
+        for (; t < a.n_steps; t++) {
+            for (int l = 0; l <= L; l++) {
+                for (int k = (l == L ? K_F : K_A); k <= (l == L ? K_F : K_E); k++) {
+                    asm volatile("" : "+v"(lane));
+                    // stream in bounded batches in every window between barriers,
+                    // so the weight stream never holds up a barrier for long
+                    top_up(q, 24, a, s_lt, s_ph, s_pst, s_pend, rw, lane);
+                    // every earlier phase is released, so this one fits; make sure
+                    // it is issued, then wait for its last DMA
+                    for (int guard = 0; q.btail <= q.bhead && guard < 64; guard++)
+                        top_up(q, 64, a, s_lt, s_ph, s_pst, s_pend, rw, lane);
+                    if (q.btail > q.bhead) wait_vm(q.issued - ufl(s_pend[q.bhead % S_NBIAS]));
+                    else atomicOr(a.err, 2);            // cannot happen: the ring holds any one phase
+                    raw_barrier();                      // B1
+                    top_up(q, 12, a, s_lt, s_ph, s_pst, s_pend, rw, lane);
+                    raw_barrier();                      // B2: the phase's slots are free again
+                    const PhaseOf p = phase_of(s_ph, k);
+                    q.head += p.n * p.R * p.ch;
+                    q.bhead++;
+                }
+            }
+            top_up(q, 24, a, s_lt, s_ph, s_pst, s_pend, rw, lane);
+            raw_barrier();                              // B3
+            if (hd[H_STOP]) { t++; break; }
+        }
+        // no LDS DMA may be in flight when the workgroup's LDS is released
+        __builtin_amdgcn_s_waitcnt(0x0f70);
+        return;
     }
-    const float *ring = reinterpret_cast<const float *>(lds + lo.ring) + (size_t)wid * lo.rs * (S_SLOT / 4);
-    const float *bslot = reinterpret_cast<const float *>(lds + lo.bias) + (size_t)wid * S_NBIAS * (S_BSLOT / 4);
+
+    // ================= compute wavefronts 1 .. S_NCW =================
+    const int cw = wid - 1;
     const int FC = ldF / 256;
+    int bhead = 0;
     int t = 0;
     for (; t < a.n_steps; t++) {
         for (int l = 0; l <= L; l++) {
             for (int k = (l == L ? K_F : K_A); k <= (l == L ? K_F : K_E); k++) {
                 asm volatile("" : "+v"(lane));
-                top_up(st, a, s_lt, s_ph, lsum, rw, lane);
-                const PhaseOf p = phase_of(s_ph, wid, l, k, lsum);
+                const PhaseOf p = phase_of(s_ph, k);
+                raw_barrier();                                   // B1: phase input staged, weights in the ring
+                const int ps = ufl(s_pst[bhead % S_NBIAS]);      // the phase's first ring slot
+                const float *bs = bslot + (bhead % S_NBIAS) * (S_BSLOT / 4);
+                float *out = s_out + (size_t)((4 * l + k) & 1) * lo.sout;
                 const int slots = p.R * p.ch;
-                raw_barrier();                                   // B1: phase input staged
-                const float *out_base = s_out + (size_t)((4 * l + k) & 1) * lo.sout;
-                if (p.m > 0) {
-                    st.done += 1;                                // the phase's bias item
-                    const float *bs = bslot + (st.bhead % S_NBIAS) * (S_BSLOT / 4);
-                    if (k == K_E) {
-                        f4 y[NB][FCMAX];
+                if (k == K_E) {
+                    f4 y[NB][FCMAX];
 #pragma unroll
-                        for (int b = 0; b < NB; b++)
+                    for (int b = 0; b < NB; b++)
 #pragma unroll
-                            for (int c = 0; c < FCMAX; c++)
-                                if (c < FC) y[b][c] = *reinterpret_cast<const f4 *>(acts + b * ldF + c * 256 + 4 * lane);
-                        for (int i = 0; i < p.m; i++) {
-                            const int hs = unit_ready(st, a, s_lt, s_ph, lsum, rw, lane, slots);
-                            f4 wv[FCMAX];
+                        for (int c = 0; c < FCMAX; c++)
+                            if (c < FC) y[b][c] = *reinterpret_cast<const f4 *>(acts + b * ldF + c * 256 + 4 * lane);
+                    int hs = ps + cw * slots;
+                    hs = hs >= lo.rs ? hs - lo.rs : hs;
+                    for (int j = cw; j < p.n; j += S_NCW) {
+                        f4 wv[FCMAX];
+#pragma unroll
+                        for (int c = 0; c < FCMAX; c++) {
+                            int sl = hs + c;
+                            sl = sl >= lo.rs ? sl - lo.rs : sl;
+                            if (c < FC) wv[c] = *reinterpret_cast<const f4 *>(ring + sl * (S_SLOT / 4) + 4 * lane);
+                        }
+                        const int n = p.u0 + j;
+                        const float bd = bs[j];
+#pragma unroll
+                        for (int b = 0; b < NB; b++) {
+                            float sum = 0.f;
 #pragma unroll
                             for (int c = 0; c < FCMAX; c++) {
-                                int sl = hs + c;
-                                sl = sl >= st.rs ? sl - st.rs : sl;
-                                if (c < FC) wv[c] = *reinterpret_cast<const f4 *>(ring + sl * (S_SLOT / 4) + 4 * lane);
+                                if (c >= FC) continue;
+                                sum += wv[c].x * y[b][c].x + wv[c].y * y[b][c].y + wv[c].z * y[b][c].z + wv[c].w * y[b][c].w;
                             }
-                            const int j = p.j0 + NCW * i, n = p.u0 + j;
-                            const float bd = bs[i];
-#pragma unroll
-                            for (int b = 0; b < NB; b++) {
-                                float sum = 0.f;
-#pragma unroll
-                                for (int c = 0; c < FCMAX; c++) {
-                                    if (c >= FC) continue;
-                                    sum += wv[c].x * y[b][c].x + wv[c].y * y[b][c].y + wv[c].z * y[b][c].z + wv[c].w * y[b][c].w;
-                                }
-                                sum = wave_sum(sum);
-                                if (lane == 0) const_cast<float *>(out_base)[b * p.n + j] = x1s[b * ldD + n] + (sum + bd);
-                            }
-                            st.head += slots;
-                            st.done += slots;
+                            sum = wave_sum(sum);
+                            if (lane == 0) out[b * p.n + j] = x1s[b * ldD + n] + (sum + bd);   // transformer.c:415
                         }
-                    } else {
-                        const float *src = k == K_C ? as : ys;
-                        f4 y[NB][DC];
-#pragma unroll
-                        for (int b = 0; b < NB; b++)
-#pragma unroll
-                            for (int c = 0; c < DC; c++) y[b][c] = *reinterpret_cast<const f4 *>(src + b * ldD + c * 256 + 4 * lane);
-                        float bv[NB];
-                        int bi[NB];
-#pragma unroll
-                        for (int b = 0; b < NB; b++) { bv[b] = -INFINITY; bi[b] = 0x7fffffff; }
-                        for (int i = 0; i < p.m; i++) {
-                            const int hs = unit_ready(st, a, s_lt, s_ph, lsum, rw, lane, slots);
-                            const int j = p.j0 + NCW * i, u = p.u0 + j;
-                            f4 wv[2][DC];
-#pragma unroll
-                            for (int r = 0; r < 2; r++)
-#pragma unroll
-                                for (int c = 0; c < DC; c++) {
-                                    if (r >= p.R) continue;
-                                    int sl = hs + r * DC + c;
-                                    sl = sl >= st.rs ? sl - st.rs : sl;
-                                    wv[r][c] = *reinterpret_cast<const f4 *>(ring + sl * (S_SLOT / 4) + 4 * lane);
-                                }
-                            float acc[2][NB];
-#pragma unroll
-                            for (int b = 0; b < NB; b++) {
-                                float s0 = 0.f, s1 = 0.f;
-#pragma unroll
-                                for (int c = 0; c < DC; c++) {
-                                    const f4 yy = y[b][c];
-                                    s0 += wv[0][c].x * yy.x + wv[0][c].y * yy.y + wv[0][c].z * yy.z + wv[0][c].w * yy.w;
-                                    if (p.R == 2)
-                                        s1 += wv[1][c].x * yy.x + wv[1][c].y * yy.y + wv[1][c].z * yy.z + wv[1][c].w * yy.w;
-                                }
-                                acc[0][b] = wave_sum(s0);
-                                acc[1][b] = p.R == 2 ? wave_sum(s1) : 0.f;
-                            }
-                            float *out = const_cast<float *>(out_base);
-                            if (k == K_A) {
-                                const float b0 = bs[2 * i], b1 = bs[2 * i + 1];
-                                const int n = 2 * u, sec = n / D, jj = (n - sec * D) % DK;
-#pragma unroll
-                                for (int b = 0; b < NB; b++) {
-                                    float v0 = acc[0][b] + b0, v1 = acc[1][b] + b1;
-                                    if (sec < 2 && a.rope) {             // rope.c:28-32
-                                        const float c = s_rope[b * 64 + jj / 2], sn = s_rope[b * 64 + 32 + jj / 2];
-                                        const float e = v0, o = v1;
-                                        v0 = e * c - o * sn;
-                                        v1 = e * sn + o * c;
-                                    }
-                                    if (lane == 0) { out[b * 2 * p.n + 2 * j] = v0; out[b * 2 * p.n + 2 * j + 1] = v1; }
-                                }
-                            } else if (k == K_C) {
-                                const float bo = bs[i];
-#pragma unroll
-                                for (int b = 0; b < NB; b++)
-                                    if (lane == 0) out[b * p.n + j] = xs[b * ldD + u] + (acc[0][b] + bo);
-                            } else if (k == K_D) {
-                                const float bg = bs[2 * i], bu = bs[2 * i + 1];
-#pragma unroll
-                                for (int b = 0; b < NB; b++) {
-                                    const float gg = acc[0][b] + bg, up = acc[1][b] + bu;
-                                    if (lane == 0) out[b * p.n + j] = (gg / (1.0f + expf(-gg))) * up;   // simd.h:394-397
-                                }
-                            } else {
-                                const float lb = bs[i];
-#pragma unroll
-                                for (int b = 0; b < NB; b++) {
-                                    const float lg = acc[0][b] + lb;
-                                    if (lg > bv[b]) { bv[b] = lg; bi[b] = u; }
-                                    if (a.logits && lane == 0) a.logits[((size_t)t * B + b) * V + u] = lg;
-                                }
-                            }
-                            st.head += slots;
-                            st.done += slots;
-                        }
-                        if (k == K_F && lane == 0) {
-#pragma unroll
-                            for (int b = 0; b < NB; b++) {
-                                s_best[(wid * MAXB + b) * 2] = bv[b];
-                                s_best[(wid * MAXB + b) * 2 + 1] = __builtin_bit_cast(float, bi[b]);
-                            }
-                        }
+                        hs += S_NCW * slots;
+                        while (hs >= lo.rs) hs -= lo.rs;
                     }
-                    st.bhead++;
-                } else if (k == K_F && lane == 0) {
+                } else {
+                    const float *src = k == K_C ? as : ys;
+                    f4 y[NB][DC];
 #pragma unroll
-                    for (int b = 0; b < NB; b++) {
-                        s_best[(wid * MAXB + b) * 2] = -INFINITY;
-                        s_best[(wid * MAXB + b) * 2 + 1] = __builtin_bit_cast(float, 0x7fffffff);
+                    for (int b = 0; b < NB; b++)
+#pragma unroll
+                        for (int c = 0; c < DC; c++) y[b][c] = *reinterpret_cast<const f4 *>(src + b * ldD + c * 256 + 4 * lane);
+                    float bv[NB];
+                    int bi[NB];
+#pragma unroll
+                    for (int b = 0; b < NB; b++) { bv[b] = -INFINITY; bi[b] = 0x7fffffff; }
+                    int hs = ps + cw * slots;
+                    hs = hs >= lo.rs ? hs - lo.rs : hs;
+                    for (int j = cw; j < p.n; j += S_NCW) {
+                        const int u = p.u0 + j;
+                        f4 wv[2][DC];
+#pragma unroll
+                        for (int r = 0; r < 2; r++)
+#pragma unroll
+                            for (int c = 0; c < DC; c++) {
+                                if (r >= p.R) continue;
+                                int sl = hs + r * DC + c;
+                                sl = sl >= lo.rs ? sl - lo.rs : sl;
+                                wv[r][c] = *reinterpret_cast<const f4 *>(ring + sl * (S_SLOT / 4) + 4 * lane);
+                            }
+                        float acc[2][NB];
+#pragma unroll
+                        for (int b = 0; b < NB; b++) {
+                            float s0 = 0.f, s1 = 0.f;
+#pragma unroll
+                            for (int c = 0; c < DC; c++) {
+                                const f4 yy = y[b][c];
+                                s0 += wv[0][c].x * yy.x + wv[0][c].y * yy.y + wv[0][c].z * yy.z + wv[0][c].w * yy.w;
+                                if (p.R == 2)
+                                    s1 += wv[1][c].x * yy.x + wv[1][c].y * yy.y + wv[1][c].z * yy.z + wv[1][c].w * yy.w;
+                            }
+                            if (p.R == 2) wave_sum2(s0, s1);
+                            else s0 = wave_sum(s0);
+                            acc[0][b] = s0;
+                            acc[1][b] = s1;
+                        }
+                        if (k == K_A) {
+                            const float b0 = bs[2 * j], b1 = bs[2 * j + 1];
+                            const int n = 2 * u, sec = n / D, jj = (n - sec * D) % DK;
+#pragma unroll
+                            for (int b = 0; b < NB; b++) {
+                                float v0 = acc[0][b] + b0, v1 = acc[1][b] + b1;
+                                if (sec < 2 && a.rope) {             // rope.c:28-32
+                                    const float c = s_rope[b * 64 + jj / 2], sn = s_rope[b * 64 + 32 + jj / 2];
+                                    const float e = v0, o = v1;
+                                    v0 = e * c - o * sn;
+                                    v1 = e * sn + o * c;
+                                }
+                                if (lane == 0) { out[b * 2 * p.n + 2 * j] = v0; out[b * 2 * p.n + 2 * j + 1] = v1; }
+                            }
+                        } else if (k == K_C) {
+                            const float bo = bs[j];
+#pragma unroll
+                            for (int b = 0; b < NB; b++)
+                                if (lane == 0) out[b * p.n + j] = xs[b * ldD + u] + (acc[0][b] + bo);   // transformer.c:408
+                        } else if (k == K_D) {
+                            const float bg = bs[j], bu = bs[32 + j];
+#pragma unroll
+                            for (int b = 0; b < NB; b++) {
+                                const float gg = acc[0][b] + bg, up = acc[1][b] + bu;
+                                if (lane == 0) out[b * p.n + j] = (gg / (1.0f + expf(-gg))) * up;   // simd.h:394-397
+                            }
+                        } else {
+                            const float lb = bs[j];
+#pragma unroll
+                            for (int b = 0; b < NB; b++) {
+                                const float lg = acc[0][b] + lb;
+                                if (lg > bv[b]) { bv[b] = lg; bi[b] = u; }
+                                if (a.logits && lane == 0) a.logits[((size_t)t * B + b) * V + u] = lg;
+                            }
+                        }
+                        hs += S_NCW * slots;
+                        while (hs >= lo.rs) hs -= lo.rs;
+                    }
+                    if (k == K_F && lane == 0) {
+#pragma unroll
+                        for (int b = 0; b < NB; b++) {
+                            s_best[(cw * MAXB + b) * 2] = bv[b];
+                            s_best[(cw * MAXB + b) * 2 + 1] = __builtin_bit_cast(float, bi[b]);
+                        }
                     }
                 }
+                bhead++;
                 raw_barrier();                                   // B2: outputs in OUT
             }
         }
-        top_up(st, a, s_lt, s_ph, lsum, rw, lane);
         raw_barrier();                                           // B3: stop flag
         if (hd[H_STOP]) { t++; break; }
     }
-    // no LDS DMA may be in flight when the workgroup's LDS is released
-    __builtin_amdgcn_s_waitcnt(0x0f70);
 }
 
 #define DNNHIP_INST5(NB, DC) template __global__ void decode_v5<NB, DC>(StreamArgs);

@@ -183,9 +183,9 @@ int pick_nb(int B) { return B > 4 ? 8 : B > 2 ? 4 : B > 1 ? 2 : 1; }
 // The streaming kernel's launch shape for this model, batch and grid, or
 // false where it does not apply (the general kernel runs instead): every GEMV
 // workgroup must own out_proj and down rows (so each takes part in every
-// layer), each compute wavefront's biases of a phase must fit one 64-lane
-// gather, the attention partials one 64-lane merge, and the weight ring must
-// hold the largest unit.
+// layer), a workgroup's biases of a phase must fit one 64-lane gather (32
+// gate + 32 up for gate/up), the attention partials one 64-lane merge, and
+// the weight ring must hold any one phase of a workgroup.
 bool stream_plan(const dnn_hip_model *m, int B, int grid, int lds_max, StreamArgs *sa) {
     if (B > 2) return false;
     const int nb = B, NS = stream_splits(nb), NA = B * m->H * NS, NG = grid - NA;
@@ -193,17 +193,19 @@ bool stream_plan(const dnn_hip_model *m, int B, int grid, int lds_max, StreamArg
     const int DC = m->ldD / LDALIGN, FC = m->ldF / LDALIGN;
     const int nu[5] = {3 * m->D / 2, m->D, m->F, m->D, m->V};
     const int R[5] = {2, 1, 2, 1, 1};
+    const int ch[5] = {DC, DC, DC, FC, DC};
+    const int bias_cap[5] = {WAVE / 2, WAVE, WAVE / 2, WAVE, WAVE};
     const int out_per_unit[4] = {2, 1, 1, 1};
-    int sout = 0;
+    int sout = 0, ring_need = 0;
     for (int k = 0; k < 5; k++) {
         const int n_wg = (nu[k] + NG - 1) / NG;
-        if ((n_wg + S_NCW - 1) / S_NCW * R[k] > WAVE) return false;
+        if (n_wg > bias_cap[k]) return false;
+        ring_need = std::max(ring_need, n_wg * R[k] * ch[k]);
         if (k < 4) sout = std::max(sout, nb * n_wg * out_per_unit[k]);
     }
     const int fixed = lds5_layout(nb, m->ldD, m->ldF, m->L, sout, 0).total;
-    int rs = (lds_max - fixed) / (S_NCW * S_SLOT);
-    rs = std::min(rs, 48);
-    if (rs < std::max(2 * DC, FC)) return false;
+    const int rs = (lds_max - fixed) / S_SLOT;
+    if (rs < ring_need) return false;
     sa->lds = lds5_layout(nb, m->ldD, m->ldF, m->L, sout, rs);
     if (sa->lds.total > lds_max) return false;
     sa->ex = Exch5{m->D, m->F, B, m->H, NS, NG};
@@ -453,93 +455,15 @@ int dnn_hip_session_last_ms(dnn_hip_session *s, float *ms) {
 
 namespace {
 
-// A session of more than MAXB rows: each group of rows decodes in turn, its
-// columns of feed / ids / logits gathered and scattered.  With eos >= 0 a
-// group that stops early is run on (greedy, no stop) to the step where the
-// last group stopped, so every row advances the same number of steps, as in
-// one launch.
-int decode_groups(dnn_hip_session *s, const int *feed, int n_feed_all, const int *n_feed, int n_steps, int eos,
-                  int *ids, float *logits, int *steps_done) {
-    const int B = s->B, V = s->m->V;
-    int nf_max = 0;
-    for (int b = 0; b < B; b++) nf_max = std::max(nf_max, n_feed ? n_feed[b] : n_feed_all);
-    std::vector<int> gfeed, gnf, gids;
-    std::vector<float> glog;
-    std::vector<int> done(s->groups.size(), 0);
-    float ms = 0.f;
-    int r0 = 0;
-    for (size_t gi = 0; gi < s->groups.size(); gi++) {
-        dnn_hip_session *g = s->groups[gi];
-        const int gb = g->B;
-        gfeed.assign((size_t)std::max(nf_max, 1) * gb, 0);
-        gnf.assign(gb, 0);
-        for (int b = 0; b < gb; b++) {
-            gnf[b] = n_feed ? n_feed[r0 + b] : n_feed_all;
-            for (int t = 0; t < gnf[b] && t < nf_max; t++) gfeed[(size_t)t * gb + b] = feed[(size_t)t * B + r0 + b];
-        }
-        gids.assign((size_t)n_steps * gb, 0);
-        if (logits) glog.assign((size_t)n_steps * gb * V, 0.f);
-        int d = 0;
-        int rc = dnn_hip_decode(g, gfeed.data(), 0, gnf.data(), n_steps, eos, gids.data(), logits ? glog.data() : nullptr, &d);
-        if (rc) return rc;
-        float gms = 0.f;
-        dnn_hip_session_last_ms(g, &gms);
-        ms += gms;
-        done[gi] = d;
-        for (int t = 0; t < d; t++)
-            for (int b = 0; b < gb; b++) {
-                if (ids) ids[(size_t)t * B + r0 + b] = gids[(size_t)t * gb + b];
-                if (logits)
-                    memcpy(logits + ((size_t)t * B + r0 + b) * V, glog.data() + ((size_t)t * gb + b) * V, sizeof(float) * V);
-            }
-        r0 += gb;
-    }
-    const int all_done = *std::max_element(done.begin(), done.end());
-    r0 = 0;
-    for (size_t gi = 0; gi < s->groups.size(); gi++) {
-        dnn_hip_session *g = s->groups[gi];
-        const int gb = g->B, more = all_done - done[gi];
-        if (more > 0) {
-            // feed each row its last id, then run greedily without a stop
-            std::vector<int> last(gb);
-            for (int b = 0; b < gb; b++) last[b] = ids ? ids[(size_t)(done[gi] - 1) * B + r0 + b] : 0;
-            gids.assign((size_t)more * gb, 0);
-            if (logits) glog.assign((size_t)more * gb * V, 0.f);
-            int rc = dnn_hip_decode(g, last.data(), 1, nullptr, more, -1, gids.data(), logits ? glog.data() : nullptr, nullptr);
-            if (rc) return rc;
-            float gms = 0.f;
-            dnn_hip_session_last_ms(g, &gms);
-            ms += gms;
-            for (int t = 0; t < more; t++)
-                for (int b = 0; b < gb; b++) {
-                    if (ids) ids[(size_t)(done[gi] + t) * B + r0 + b] = gids[(size_t)t * gb + b];
-                    if (logits)
-                        memcpy(logits + ((size_t)(done[gi] + t) * B + r0 + b) * V, glog.data() + ((size_t)t * gb + b) * V,
-                               sizeof(float) * V);
-                }
-        }
-        r0 += gb;
-    }
-    s->last_ms = ms;
-    if (steps_done) *steps_done = all_done;
-    return DNN_HIP_OK;
-}
-
-}  // namespace
-
-int dnn_hip_decode(dnn_hip_session *s, const int *feed, int n_feed_all, const int *n_feed,
-                   int n_steps, int eos, int *ids, float *logits, int *steps_done) {
-    if (!s || !feed) return fail(DNN_HIP_EINVAL, "NULL argument");
+// Validate and enqueue one launch of a session of at most MAXB rows on its
+// stream (grid capped at grid_limit when > 0); decode_finish waits for it.
+// check_only: validate the arguments, enqueue nothing.  prep: the session is
+// one group of a multi-group launch: upload its inputs, fill *prep with its
+// kernel arguments (general kernel, MAXB-row build) and launch nothing.
+int decode_launch(dnn_hip_session *s, const int *feed, int n_feed_all, const int *n_feed, int n_steps, int eos,
+                  bool want_logits, int grid_limit, bool check_only = false, DecodeArgs *prep = nullptr) {
     dnn_hip_model *m = s->m;
     const int B = s->B;
-    if (n_steps <= 0) return fail(DNN_HIP_EINVAL, "n_steps %d", n_steps);
-    if (!s->groups.empty()) {
-        if (!ids && eos >= 0) return fail(DNN_HIP_EINVAL, "a multi-group session needs ids when eos >= 0");
-        for (int b = 0; b < B; b++)
-            if ((n_feed ? n_feed[b] : n_feed_all) < 1)
-                return fail(DNN_HIP_EINVAL, "row %d: n_feed %d < 1", b, n_feed ? n_feed[b] : n_feed_all);
-        return decode_groups(s, feed, n_feed_all, n_feed, n_steps, eos, ids, logits, steps_done);
-    }
     std::vector<int> nf(B);
     int nf_max = 0;
     for (int b = 0; b < B; b++) {
@@ -558,13 +482,15 @@ int dnn_hip_decode(dnn_hip_session *s, const int *feed, int n_feed_all, const in
         if (m->rope && s->h_pos[b] + n_steps > m->rope_rows)
             return fail(DNN_HIP_ERANGE, "row %d: position %d beyond the RoPE table (%d rows)", b, s->h_pos[b] + n_steps - 1, m->rope_rows);
     }
+    if (check_only) return DNN_HIP_OK;
     const int dc = m->ldD / LDALIGN;
-    const int nb = pick_nb(B);
+    const int nb = prep ? MAXB : pick_nb(B);
     HIP_TRY(hipSetDevice(m->device));
     int lds_max = 0;
     HIP_TRY(hipDeviceGetAttribute(&lds_max, hipDeviceAttributeMaxSharedMemoryPerBlock, m->device));
     int grid = s->grid_cap;
     if (s->grid_req > 0) grid = std::min(grid, s->grid_req);
+    if (grid_limit > 0) grid = std::min(grid, grid_limit);
     // decode_v3 by default; the lookahead kernel (one or two rows) on request,
     // when its schedule fits (every GEMV round in at most 3 slots of the grid's
     // non-attention workgroups) and its LDS does.
@@ -572,14 +498,17 @@ int dnn_hip_decode(dnn_hip_session *s, const int *feed, int n_feed_all, const in
     size_t shmem = 0;
     StreamArgs sa{};
     bool stream = false;
-    if (s->kernel_pref == 5 && stream_plan(m, B, grid, lds_max, &sa) &&
+    if (prep) {
+        kern = decode_multi_for(dc);
+        shmem = lds_bytes(nb, m->ldD, m->ldF);
+    } else if (s->kernel_pref == 5 && stream_plan(m, B, grid, lds_max, &sa) &&
         sa.ex.total(m->L) <= s->xa_pairs) {
         kern = decode_stream_for(nb, dc);
         shmem = (size_t)sa.lds.total;
         stream = kern != nullptr;
     }
     const int rounds = (m->D + 6) / 7 + (3 * m->D / 2 + 6) / 7 + (m->D / 2 + 6) / 7 + (m->F + 6) / 7;
-    if (!kern && nb <= 2 && s->kernel_pref == 4 && grid > B * m->H && rounds <= 3 * (grid - B * m->H) &&
+    if (!kern && !prep && nb <= 2 && s->kernel_pref == 4 && grid > B * m->H && rounds <= 3 * (grid - B * m->H) &&
         lds4_bytes(nb, m->ldD, m->ldF, m->L) <= (size_t)lds_max) {
         kern = decode_lookahead_for(nb, dc);
         shmem = lds4_bytes(nb, m->ldD, m->ldF, m->L);
@@ -589,10 +518,10 @@ int dnn_hip_decode(dnn_hip_session *s, const int *feed, int n_feed_all, const in
         shmem = lds_bytes(nb, m->ldD, m->ldF);
     }
     if (!kern) return fail(DNN_HIP_EINVAL, "d_model %d: the decode kernels cover d_model <= %d", m->D, 3 * LDALIGN);
-    s->kernel_used = stream ? 5 : kern == decode_kernel_for(nb, dc) ? 3 : 4;
+    s->kernel_used = stream ? 5 : (prep || kern == decode_kernel_for(nb, dc)) ? 3 : 4;
     int rc = grow(&s->feed, &s->feed_cap, (size_t)nf_max * B);
     if (!rc) rc = grow(&s->ids, &s->ids_cap, (size_t)n_steps * B);
-    if (!rc && logits) rc = grow(&s->logits, &s->logits_cap, (size_t)n_steps * B * m->V);
+    if (!rc && want_logits) rc = grow(&s->logits, &s->logits_cap, (size_t)n_steps * B * m->V);
     if (rc) return rc;
     HIP_TRY(hipMemcpyAsync(s->feed, feed, sizeof(int) * (size_t)nf_max * B, hipMemcpyHostToDevice, s->stream));
     HIP_TRY(hipMemcpyAsync(s->n_feed, nf.data(), sizeof(int) * B, hipMemcpyHostToDevice, s->stream));
@@ -625,16 +554,31 @@ int dnn_hip_decode(dnn_hip_session *s, const int *feed, int n_feed_all, const in
     a.kc = s->kc; a.vc = s->vc; a.xa = s->xa; a.ex = s->ex;
     a.ex.grid = s->grid_cap;
     a.pos = s->pos; a.feed = s->feed; a.n_feed = s->n_feed;
-    a.ids = s->ids; a.logits = logits ? s->logits : nullptr;
+    a.ids = s->ids; a.logits = want_logits ? s->logits : nullptr;
     a.n_steps = n_steps; a.eos = eos; a.step0 = s->next_tag; a.err = s->err; a.steps_done = s->steps_done;
     s->next_tag += (unsigned)n_steps;
+    if (prep) {
+        *prep = a;
+        HIP_TRY(hipStreamSynchronize(s->stream));   // inputs in place before the shared launch
+        return DNN_HIP_OK;
+    }
     sa.a = a;
     void *kargs[] = {stream ? static_cast<void *>(&sa) : static_cast<void *>(&a)};
     HIP_TRY(hipEventRecord(s->ev0, s->stream));
     HIP_TRY(hipLaunchKernel(kern, dim3(grid), dim3(BLOCK), kargs, shmem, s->stream));
     HIP_TRY(hipEventRecord(s->ev1, s->stream));
-    HIP_TRY(hipEventSynchronize(s->ev1));
-    HIP_TRY(hipEventElapsedTime(&s->last_ms, s->ev0, s->ev1));
+    return DNN_HIP_OK;
+}
+
+// timed: the launch was the session's own (its events bracket it); otherwise
+// the caller has synchronised the shared launch.
+int decode_finish(dnn_hip_session *s, int *ids, float *logits, int *steps_done, bool timed = true) {
+    dnn_hip_model *m = s->m;
+    const int B = s->B;
+    if (timed) {
+        HIP_TRY(hipEventSynchronize(s->ev1));
+        HIP_TRY(hipEventElapsedTime(&s->last_ms, s->ev0, s->ev1));
+    }
     int done = 0, kerr = 0;
     HIP_TRY(hipMemcpy(&kerr, s->err, sizeof(int), hipMemcpyDeviceToHost));
     if (kerr) return fail(DNN_HIP_EDEVICE, "decode kernel: a dependency wait timed out (error bits %#x); results discarded", kerr);
@@ -644,6 +588,127 @@ int dnn_hip_decode(dnn_hip_session *s, const int *feed, int n_feed_all, const in
     HIP_TRY(hipMemcpy(s->h_pos.data(), s->pos, sizeof(int) * B, hipMemcpyDeviceToHost));
     if (steps_done) *steps_done = done;
     return DNN_HIP_OK;
+}
+
+int decode_finish_launch(dnn_hip_session *s, const int *feed, int n_feed_all, const int *n_feed, int n_steps, int eos,
+                         int *ids, float *logits, int *steps_done) {
+    const int rc = decode_launch(s, feed, n_feed_all, n_feed, n_steps, eos, logits != nullptr, 0);
+    return rc ? rc : decode_finish(s, ids, logits, steps_done);
+}
+
+// A session of more than MAXB rows: its groups of at most MAXB rows decode in
+// one launch of the general kernel, the grid split evenly between them
+// (persistent launches on separate streams are not co-resident on this
+// device, so a launch per group would run them in turn); the columns of feed /
+// ids / logits are gathered and scattered per group.  With eos >= 0 a group
+// that stops early is run on (greedy, no stop) to the step where the last
+// group stopped, so every row advances the same number of steps, as in one
+// launch.
+int decode_groups(dnn_hip_session *s, const int *feed, int n_feed_all, const int *n_feed, int n_steps, int eos,
+                  int *ids, float *logits, int *steps_done) {
+    const int B = s->B, V = s->m->V, NGR = (int)s->groups.size();
+    int nf_max = 0;
+    for (int b = 0; b < B; b++) nf_max = std::max(nf_max, n_feed ? n_feed[b] : n_feed_all);
+    std::vector<std::vector<int>> gfeed(NGR), gnf(NGR), gids(NGR);
+    std::vector<std::vector<float>> glog(NGR);
+    std::vector<int> r0(NGR), done(NGR, 0), more(NGR, 0);
+    for (int gi = 0, r = 0; gi < NGR; gi++) { r0[gi] = r; r += s->groups[gi]->B; }
+    dnn_hip_session *lead = s->groups[0];
+    dnn_hip_model *m = s->m;
+    float ms = 0.f;
+    // pass 0: every group from its feed; pass 1: groups that stopped early, run on
+    for (int pass = 0; pass < 2; pass++) {
+        if (pass == 1) {
+            const int all_done = *std::max_element(done.begin(), done.end());
+            for (int gi = 0; gi < NGR; gi++) more[gi] = all_done - done[gi];
+        }
+        std::vector<int> run;
+        for (int gi = 0; gi < NGR; gi++) {
+            const int gb = s->groups[gi]->B;
+            if (pass == 0) {
+                gfeed[gi].assign((size_t)std::max(nf_max, 1) * gb, 0);
+                gnf[gi].assign(gb, 0);
+                for (int b = 0; b < gb; b++) {
+                    gnf[gi][b] = n_feed ? n_feed[r0[gi] + b] : n_feed_all;
+                    for (int t = 0; t < gnf[gi][b] && t < nf_max; t++)
+                        gfeed[gi][(size_t)t * gb + b] = feed[(size_t)t * B + r0[gi] + b];
+                }
+                run.push_back(gi);
+            } else if (more[gi] > 0) {
+                // feed each row its last id, then run greedily without a stop
+                gfeed[gi].assign(gb, 0);
+                gnf[gi].assign(gb, 1);
+                for (int b = 0; b < gb; b++) gfeed[gi][b] = ids[(size_t)(done[gi] - 1) * B + r0[gi] + b];
+                run.push_back(gi);
+            }
+        }
+        if (run.empty()) continue;
+        const int per = std::max(1, lead->grid_cap / (int)run.size());
+        // every group is validated before any input is uploaded
+        for (int gi : run) {
+            const int rc = decode_launch(s->groups[gi], gfeed[gi].data(), 0, gnf[gi].data(), pass == 0 ? n_steps : more[gi],
+                                         pass == 0 ? eos : -1, logits != nullptr, per, true);
+            if (rc) return rc;
+        }
+        MultiArgs ma{};
+        ma.n = (int)run.size();
+        ma.per = per;
+        for (int i = 0; i < ma.n; i++) {
+            const int gi = run[i];
+            const int rc = decode_launch(s->groups[gi], gfeed[gi].data(), 0, gnf[gi].data(), pass == 0 ? n_steps : more[gi],
+                                         pass == 0 ? eos : -1, logits != nullptr, per, false, &ma.a[i]);
+            if (rc) return rc;
+        }
+        const void *kern = decode_multi_for(m->ldD / LDALIGN);
+        const size_t shmem = lds_bytes(MAXB, m->ldD, m->ldF);
+        void *kargs[] = {&ma};
+        HIP_TRY(hipEventRecord(lead->ev0, lead->stream));
+        HIP_TRY(hipLaunchKernel(kern, dim3(per * ma.n), dim3(BLOCK), kargs, shmem, lead->stream));
+        HIP_TRY(hipEventRecord(lead->ev1, lead->stream));
+        HIP_TRY(hipEventSynchronize(lead->ev1));
+        float pass_ms = 0.f;
+        HIP_TRY(hipEventElapsedTime(&pass_ms, lead->ev0, lead->ev1));
+        ms += pass_ms;
+        for (int gi : run) {
+            dnn_hip_session *g = s->groups[gi];
+            const int gb = g->B, steps = pass == 0 ? n_steps : more[gi];
+            gids[gi].assign((size_t)steps * gb, 0);
+            if (logits) glog[gi].assign((size_t)steps * gb * V, 0.f);
+            int d = 0;
+            const int rc = decode_finish(g, gids[gi].data(), logits ? glog[gi].data() : nullptr, &d, false);
+            if (rc) return rc;
+            g->last_ms = pass_ms;
+            const int t0 = pass == 0 ? 0 : done[gi];
+            for (int t = 0; t < d; t++)
+                for (int b = 0; b < gb; b++) {
+                    if (ids) ids[(size_t)(t0 + t) * B + r0[gi] + b] = gids[gi][(size_t)t * gb + b];
+                    if (logits)
+                        memcpy(logits + ((size_t)(t0 + t) * B + r0[gi] + b) * V, glog[gi].data() + ((size_t)t * gb + b) * V,
+                               sizeof(float) * V);
+                }
+            if (pass == 0) done[gi] = d;
+        }
+    }
+    s->last_ms = ms;
+    if (steps_done) *steps_done = *std::max_element(done.begin(), done.end());
+    return DNN_HIP_OK;
+}
+
+}  // namespace
+
+int dnn_hip_decode(dnn_hip_session *s, const int *feed, int n_feed_all, const int *n_feed,
+                   int n_steps, int eos, int *ids, float *logits, int *steps_done) {
+    if (!s || !feed) return fail(DNN_HIP_EINVAL, "NULL argument");
+    const int B = s->B;
+    if (n_steps <= 0) return fail(DNN_HIP_EINVAL, "n_steps %d", n_steps);
+    if (!s->groups.empty()) {
+        if (!ids && eos >= 0) return fail(DNN_HIP_EINVAL, "a multi-group session needs ids when eos >= 0");
+        for (int b = 0; b < B; b++)
+            if ((n_feed ? n_feed[b] : n_feed_all) < 1)
+                return fail(DNN_HIP_EINVAL, "row %d: n_feed %d < 1", b, n_feed ? n_feed[b] : n_feed_all);
+        return decode_groups(s, feed, n_feed_all, n_feed, n_steps, eos, ids, logits, steps_done);
+    }
+    return decode_finish_launch(s, feed, n_feed_all, n_feed, n_steps, eos, ids, logits, steps_done);
 }
 
 int dnn_hip_generate(dnn_hip_model *m, const int *prompt, int P, int max_new, int eos, int *out, int *n_out) {

@@ -83,8 +83,9 @@ int dnn_hip_model_destroy(dnn_hip_model *m);
 /* A decode session: the per-layer KV caches of `batch` rows in HBM (K stored
  * transposed, [L][B][H][d_k][max_seq]; V as [L][B][H][max_seq][d_k]) plus the
  * exchange arena of the decode kernel.  Every row starts empty.
- * 1 <= batch <= 64.  A launch serves at most 8 rows: a larger session holds
- * groups of at most 8 rows, decoded one after another by dnn_hip_decode. */
+ * 1 <= batch <= 64.  A session of more than 8 rows holds groups of at most
+ * 8 rows; dnn_hip_decode runs them in one launch, the grid split between
+ * them. */
 int dnn_hip_session_create(dnn_hip_model *m, int batch, int max_seq,
                            dnn_hip_session **out);
 /* Empties every row (lengths back to 0). */
