@@ -34,7 +34,8 @@ CONFIGS = {
     "c2b8": (8192, 768, 12, 12, 2048, 32, 8),
 }
 SEED = {"c1": 1, "c2": 2, "c3": 3, "c2b8": 2}
-KERNELS = {3: "decode_v3<NB,DC>", 4: "decode_v4<NB,DC>", 5: "decode_v5<NB,DC>"}
+KERNELS = {3: "decode_v3<NB,DC>", 4: "decode_v4<NB,DC>", 5: "decode_v5<NB,DC>",
+           6: "batched engine: gemm_kernel / attn_kernel chain, one HIP graph replay per step"}
 
 
 class Ctx(C.Structure):

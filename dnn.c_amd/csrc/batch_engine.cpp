@@ -1,0 +1,410 @@
+// batch_engine.cpp -- host side of the batched engine: buffers, the HIP graph
+// of one decode step, multi-token prefill.
+//
+// Decode (dnn_hip_decode on a batched session) replays the captured step once
+// per token: the per-step values (positions, the step counter, the next
+// token's embedding row, the done flag) live in device memory and are advanced
+// by the last workgroup of the lm_head kernel, so one graph serves every step.
+// The graph holds no memset nodes: counters are reset by the kernels that use
+// them.
+//
+// Prefill (dnn_hip_prefill) runs the new rows of every sequence through the
+// layers at once -- the multi-token cached forward of the reference
+// (transformer_block_forward_cached_ex, transformer.c:211-416, causal or
+// prefix-LM), as decoder_lm_generate's prompt loop (gpt.c:306-344) and
+// vision_lm_generate's prefix prefill (vlm.c:497-517) need it -- and returns the
+// greedy token of each sequence's last new row.
+#include <algorithm>
+#include <cstring>
+#include <vector>
+
+#include "session.h"
+
+using namespace dnnhip;
+
+namespace {
+
+constexpr int CNT_GEMM = 4096;           // last-arriver counters of GEMM column tiles
+constexpr int CNT_ATT = MAX_ROWS * 64;   // (row, head) pairs of the decode attention
+constexpr int CNT_TOTAL = CNT_GEMM + CNT_ATT + 1;
+
+#define HIP_TRY(expr)                                                                          \
+    do {                                                                                       \
+        hipError_t e_ = (expr);                                                                \
+        if (e_ != hipSuccess)                                                                  \
+            return set_error(DNN_HIP_EDEVICE, "%s failed: %s", #expr, hipGetErrorString(e_)); \
+    } while (0)
+
+inline int round_up(int v, int a) { return (v + a - 1) / a * a; }
+
+// workgroups per column tile of a decode GEMM: every wavefront's k-steps a
+// multiple of 4 (the kernel's unroll), at least 256 workgroups where possible
+int pick_ks(int ntiles, int K) {
+    const int nks = K / 16;
+    int best = 1;
+    for (int ks = 1; ks <= 8; ks++) {
+        if (nks % (16 * ks)) continue;
+        best = ks;
+        if (ntiles * ks >= 256) break;
+    }
+    return best;
+}
+
+int attn_splits(int M, int H) { return std::max(1, std::min(8, 768 / (M * H))); }
+
+void free_acts(BatchEngine *e) {
+    float *bufs[] = {e->X, e->X1, e->ATT, e->Q, e->ACT};
+    for (float *p : bufs)
+        if (p) (void)hipFree(p);
+    e->X = e->X1 = e->ATT = e->Q = e->ACT = nullptr;
+    e->mcap = 0;
+}
+
+void drop_graph(BatchEngine *e) {
+    if (e->gexec) (void)hipGraphExecDestroy(e->gexec);
+    e->gexec = nullptr;
+    e->gkey[0] = e->gkey[1] = e->gkey[2] = e->gkey[3] = nullptr;
+}
+
+// The session's engine with activation buffers of at least `rows` rows.
+int engine_get(dnn_hip_session *s, int rows) {
+    dnn_hip_model *m = s->m;
+    if (m->L * 5 + 1 >= 128) return set_error(DNN_HIP_EINVAL, "%d layers: the batched engine covers up to 25", m->L);
+    if (m->H > 64) return set_error(DNN_HIP_EINVAL, "%d heads: the batched engine covers up to 64", m->H);
+    if (m->V > 65535) return set_error(DNN_HIP_EINVAL, "vocab %d: the batched engine covers up to 65535", m->V);
+    BatchEngine *e = s->eng;
+    if (!e) {
+        e = s->eng = new BatchEngine();
+        const int ntn_head = (m->V + 15) / 16;
+        const int ks_max = 8;
+        e->part_pairs = (size_t)ks_max * MAX_ROWS * m->D;
+        e->apart_pairs = (size_t)MAX_ROWS * m->H * 8 * (BK_DK + 2);
+        e->amax_pairs = (size_t)MAX_ROWS * ntn_head;
+        int rc = 0;
+        rc = rc ? rc : dalloc(&e->part, e->part_pairs);
+        rc = rc ? rc : dalloc(&e->apart, e->apart_pairs);
+        rc = rc ? rc : dalloc(&e->amax, e->amax_pairs);
+        rc = rc ? rc : dalloc(&e->cnt, CNT_TOTAL);
+        rc = rc ? rc : dalloc(&e->st, 1);
+        rc = rc ? rc : dalloc(&e->row_ident, MAX_ROWS);
+        rc = rc ? rc : dalloc(&e->row_done, MAX_ROWS);
+        rc = rc ? rc : dalloc(&e->steps_done, 1);
+        rc = rc ? rc : dalloc(&e->next_ids, MAX_ROWS);
+        rc = rc ? rc : dalloc(&e->pre_logits, (size_t)MAX_ROWS * m->V);
+        if (rc) return rc;
+        std::vector<int> ident(MAX_ROWS);
+        for (int i = 0; i < MAX_ROWS; i++) ident[i] = i;
+        StepState st0{1u, 0, 0, 0};   // tag 0 marks the zeroed partial buffers: never current
+        HIP_TRY(hipMemset(e->part, 0, e->part_pairs * sizeof(uint2)));
+        HIP_TRY(hipMemset(e->apart, 0, e->apart_pairs * sizeof(uint2)));
+        HIP_TRY(hipMemset(e->amax, 0, e->amax_pairs * sizeof(uint2)));
+        HIP_TRY(hipMemset(e->cnt, 0, CNT_TOTAL * sizeof(unsigned)));
+        HIP_TRY(hipMemset(e->row_done, 0, MAX_ROWS * sizeof(int)));
+        HIP_TRY(hipMemcpy(e->row_ident, ident.data(), MAX_ROWS * sizeof(int), hipMemcpyHostToDevice));
+        HIP_TRY(hipMemcpy(e->st, &st0, sizeof st0, hipMemcpyHostToDevice));
+    }
+    if (rows > e->mcap) {
+        drop_graph(e);
+        free_acts(e);
+        const int mc = round_up(std::max(rows, BK_MAXM), BK_PBM);
+        const size_t ldD = m->ldD, ldF = m->ldF;
+        int rc = 0;
+        rc = rc ? rc : dalloc(&e->X, mc * ldD);
+        rc = rc ? rc : dalloc(&e->X1, mc * ldD);
+        rc = rc ? rc : dalloc(&e->ATT, mc * ldD);
+        rc = rc ? rc : dalloc(&e->Q, mc * (size_t)m->D);
+        rc = rc ? rc : dalloc(&e->ACT, mc * ldF);
+        if (rc) { free_acts(e); return rc; }
+        // padding columns (past d_model / d_ffn) stay zero: they meet the
+        // weights' zero padding in the k-loops
+        HIP_TRY(hipMemset(e->X, 0, mc * ldD * 4));
+        HIP_TRY(hipMemset(e->X1, 0, mc * ldD * 4));
+        HIP_TRY(hipMemset(e->ATT, 0, mc * ldD * 4));
+        HIP_TRY(hipMemset(e->Q, 0, mc * (size_t)m->D * 4));
+        HIP_TRY(hipMemset(e->ACT, 0, mc * ldF * 4));
+        e->mcap = mc;
+    }
+    return DNN_HIP_OK;
+}
+
+struct Wts {
+    const dnn_hip_model *m;
+    const float *f(uint32_t off) const { return reinterpret_cast<const float *>(m->arena) + off; }
+    const void *w(uint32_t off) const {
+        return m->bf16 ? static_cast<const void *>(m->arena16 + off) : static_cast<const void *>(f(off));
+    }
+    size_t w_bytes(uint32_t off) const {
+        const size_t es = m->bf16 ? 2 : 4;
+        return (m->arena_bytes / 4 - off) * es;
+    }
+};
+
+GemmArgs gemm_base(dnn_hip_session *s, const Wts &W, uint32_t woff, int ldw, int N, int K) {
+    GemmArgs g{};
+    g.W = W.w(woff);
+    g.w_bytes = W.w_bytes(woff);
+    g.ldw = ldw;
+    g.N = N;
+    g.K = K;
+    g.ks = 1;
+    g.st = s->eng->st;
+    g.mpad = s->eng->mcap;
+    g.D = s->m->D;
+    return g;
+}
+
+// The launches of one layer: QKV, attention, out_proj, gate/up, down.  decode:
+// M = the session's rows, the attention of each row over its cache; prefill:
+// M = the packed new rows (pi: host-side prefill plan in device memory).
+struct PrefillPlan {
+    int M;
+    const int *row_b, *row_p, *pid, *row0, *n_new, *p0, *arow, *tiles;
+    int n_tiles, mode, prefix_len;
+};
+
+int enqueue_layer(dnn_hip_session *s, int l, const PrefillPlan *pp) {
+    dnn_hip_model *m = s->m;
+    BatchEngine *e = s->eng;
+    const Wts W{m};
+    const LayerOff &lo = m->h_layers[l];
+    const int D = m->D, ldD = m->ldD, ldF = m->ldF;
+    const bool pre = pp != nullptr;
+    const int M = pre ? pp->M : s->B;
+    const bool bf = m->bf16 != 0;
+
+    GemmArgs g = gemm_base(s, W, lo.wqkv, ldD, 3 * D, ldD);
+    g.A = e->X; g.lda = ldD; g.M = M;
+    g.bias = W.f(lo.bqkv);
+    g.gamma = W.f(lo.g_attn); g.eps = lo.eps_attn; g.dnorm = D;
+    g.q = e->Q; g.kc = s->kc; g.vc = s->vc;
+    g.row_b = pre ? pp->row_b : e->row_ident;
+    g.row_p = pre ? pp->row_p : s->pos;
+    g.H = m->H; g.kv_s = s->kv_s; g.B = s->B; g.layer = l;
+    g.rope = m->rope; g.rope_rows = m->rope_rows;
+    g.kslot = 5 * l;
+    HIP_TRY(launch_gemm(EPI_QKV, true, bf, pre, g, s->stream));
+
+    if (pre) {
+        PrefillAttnArgs a{};
+        a.q = e->Q; a.att = e->ATT; a.kc = s->kc; a.vc = s->vc;
+        a.row0 = pp->row0; a.n_new = pp->n_new; a.p0 = pp->p0; a.tiles = pp->tiles;
+        a.n_tiles = pp->n_tiles; a.H = m->H; a.kv_s = s->kv_s; a.layer = l; a.D = D; a.B = s->B; a.ldatt = ldD;
+        a.mode = pp->mode; a.prefix_len = pp->prefix_len; a.st = e->st;
+        HIP_TRY(launch_prefill_attn(a, s->stream));
+    } else {
+        AttnArgs a{};
+        a.q = e->Q; a.att = e->ATT; a.kc = s->kc; a.vc = s->vc; a.pos = s->pos;
+        a.M = M; a.H = m->H; a.kv_s = s->kv_s; a.layer = l; a.D = D; a.B = s->B; a.ldatt = ldD;
+        a.nsplit = attn_splits(M, m->H);
+        a.part = e->apart; a.cnt = e->cnt + CNT_GEMM; a.st = e->st; a.kslot = 5 * l + 1;
+        HIP_TRY(launch_attn(a, s->stream));
+    }
+
+    g = gemm_base(s, W, lo.wo, ldD, D, ldD);
+    g.A = e->ATT; g.lda = ldD; g.M = M;
+    g.bias = W.f(lo.bo);
+    g.out = e->X1; g.ldo = ldD; g.res = e->X; g.ldr = ldD;
+    g.ks = pre ? 1 : pick_ks((D + 15) / 16, ldD);
+    g.part = e->part; g.cnt = e->cnt; g.kslot = 5 * l + 2;
+    HIP_TRY(launch_gemm(EPI_RES, false, bf, pre, g, s->stream));
+
+    g = gemm_base(s, W, lo.wgu, ldD, 2 * m->F, ldD);
+    g.A = e->X1; g.lda = ldD; g.M = M;
+    g.bias = W.f(lo.bg); g.bias2 = W.f(lo.bu);
+    g.gamma = W.f(lo.g_ffn); g.eps = lo.eps_ffn; g.dnorm = D;
+    g.out = e->ACT; g.ldo = ldF;
+    g.kslot = 5 * l + 3;
+    HIP_TRY(launch_gemm(EPI_SWIGLU, true, bf, pre, g, s->stream));
+
+    g = gemm_base(s, W, lo.wd, ldF, D, ldF);
+    g.A = e->ACT; g.lda = ldF; g.M = M;
+    g.bias = W.f(lo.bd);
+    g.out = e->X; g.ldo = ldD; g.res = e->X1; g.ldr = ldD;
+    g.ks = pre ? 1 : pick_ks((D + 15) / 16, ldF);
+    g.part = e->part; g.cnt = e->cnt; g.kslot = 5 * l + 4;
+    HIP_TRY(launch_gemm(EPI_RES, false, bf, pre, g, s->stream));
+    return DNN_HIP_OK;
+}
+
+// final rms_norm -> tied lm_head -> argmax (+ the next step's feed in decode)
+int enqueue_head(dnn_hip_session *s, const PrefillPlan *pp, float *logits, int *ids, int eos) {
+    dnn_hip_model *m = s->m;
+    BatchEngine *e = s->eng;
+    const Wts W{m};
+    const uint32_t embed = (uint32_t)(m->off.embed / 4), lm_bias = (uint32_t)(m->off.lm_bias / 4),
+                   g_final = (uint32_t)(m->off.g_final / 4);
+    GemmArgs g = gemm_base(s, W, embed, m->ldD, m->V, m->ldD);
+    g.A = e->X; g.lda = m->ldD; g.M = s->B;
+    g.arow = pp ? pp->arow : nullptr;
+    g.bias = W.f(lm_bias);
+    g.gamma = W.f(g_final); g.eps = m->eps_final; g.dnorm = m->D;
+    g.amax = e->amax; g.head_cnt = e->cnt + CNT_GEMM + CNT_ATT;
+    g.logits = logits; g.ids = ids;
+    g.feed = s->feed; g.n_feed = s->n_feed; g.pos = s->pos;
+    g.x_next = e->X; g.ldx = m->ldD; g.embed = W.f(embed);
+    g.steps_done = e->steps_done; g.eos = eos; g.row_done = e->row_done;
+    g.prefill = pp != nullptr;
+    g.kslot = 5 * m->L;
+    HIP_TRY(launch_gemm(EPI_HEAD, true, m->bf16 != 0, false, g, s->stream));
+    return DNN_HIP_OK;
+}
+
+}  // namespace
+
+namespace dnnhip {
+
+void engine_destroy(BatchEngine *e) {
+    if (!e) return;
+    drop_graph(e);
+    free_acts(e);
+    void *bufs[] = {e->part, e->apart, e->amax, e->cnt, e->st, e->row_ident, e->row_done,
+                    e->steps_done, e->pre_i, e->next_ids, e->pre_logits};
+    for (void *p : bufs)
+        if (p) (void)hipFree(p);
+    delete e;
+}
+
+int engine_decode(dnn_hip_session *s, const int *feed, int n_feed_all, const int *n_feed, int n_steps, int eos,
+                  int *ids, float *logits, int *steps_done) {
+    dnn_hip_model *m = s->m;
+    const int B = s->B;
+    std::vector<int> nf;
+    int nf_max = 0;
+    int rc = check_decode(s, feed, n_feed_all, n_feed, n_steps, nf, &nf_max);
+    if (rc) return rc;
+    HIP_TRY(hipSetDevice(m->device));
+    rc = engine_get(s, round_up(B, 16));
+    if (!rc) rc = grow(&s->feed, &s->feed_cap, (size_t)nf_max * B);
+    if (!rc) rc = grow(&s->ids, &s->ids_cap, (size_t)n_steps * B);
+    if (!rc && logits) rc = grow(&s->logits, &s->logits_cap, (size_t)n_steps * B * m->V);
+    if (rc) return rc;
+    BatchEngine *e = s->eng;
+    HIP_TRY(hipMemcpyAsync(s->feed, feed, sizeof(int) * (size_t)nf_max * B, hipMemcpyHostToDevice, s->stream));
+    HIP_TRY(hipMemcpyAsync(s->n_feed, nf.data(), sizeof(int) * B, hipMemcpyHostToDevice, s->stream));
+
+    // the step graph, captured again when a buffer it names changed
+    float *lg = logits ? s->logits : nullptr;
+    const void *key[4] = {s->feed, s->ids, lg, e->X};
+    if (!e->gexec || e->geos != eos || memcmp(key, e->gkey, sizeof key) != 0) {
+        drop_graph(e);
+        HIP_TRY(hipStreamBeginCapture(s->stream, hipStreamCaptureModeThreadLocal));
+        int erc = 0;
+        for (int l = 0; l < m->L && !erc; l++) erc = enqueue_layer(s, l, nullptr);
+        if (!erc) erc = enqueue_head(s, nullptr, lg, s->ids, eos);
+        hipGraph_t graph = nullptr;
+        const hipError_t ce = hipStreamEndCapture(s->stream, &graph);
+        if (erc) { if (graph) (void)hipGraphDestroy(graph); return erc; }
+        if (ce != hipSuccess) return set_error(DNN_HIP_EDEVICE, "step graph capture: %s", hipGetErrorString(ce));
+        const hipError_t ie = hipGraphInstantiate(&e->gexec, graph, nullptr, nullptr, 0);
+        (void)hipGraphDestroy(graph);
+        if (ie != hipSuccess) { e->gexec = nullptr; return set_error(DNN_HIP_EDEVICE, "step graph: %s", hipGetErrorString(ie)); }
+        memcpy(e->gkey, key, sizeof key);
+        e->geos = eos;
+    }
+    // the first step's embedding rows; resets the step counter, done flags
+    EmbedArgs ea{};
+    ea.embed = reinterpret_cast<const float *>(m->arena) + m->off.embed / 4;
+    ea.ids = s->feed; ea.out = e->X; ea.M = B; ea.ld = m->ldD; ea.D = m->D; ea.st = e->st; ea.row_done = e->row_done;
+    HIP_TRY(launch_embed(ea, s->stream));
+    HIP_TRY(hipEventRecord(s->ev0, s->stream));
+    for (int t = 0; t < n_steps; t++) HIP_TRY(hipGraphLaunch(e->gexec, s->stream));
+    HIP_TRY(hipEventRecord(s->ev1, s->stream));
+    HIP_TRY(hipEventSynchronize(s->ev1));
+    HIP_TRY(hipEventElapsedTime(&s->last_ms, s->ev0, s->ev1));
+    s->kernel_used = 6;
+    int done = 0;
+    HIP_TRY(hipMemcpy(&done, e->steps_done, sizeof(int), hipMemcpyDeviceToHost));
+    if (done < 1 || done > n_steps) return set_error(DNN_HIP_EDEVICE, "batched decode: %d of %d steps reported", done, n_steps);
+    if (ids) HIP_TRY(hipMemcpy(ids, s->ids, sizeof(int) * (size_t)done * B, hipMemcpyDeviceToHost));
+    if (logits) HIP_TRY(hipMemcpy(logits, s->logits, sizeof(float) * (size_t)done * B * m->V, hipMemcpyDeviceToHost));
+    HIP_TRY(hipMemcpy(s->h_pos.data(), s->pos, sizeof(int) * B, hipMemcpyDeviceToHost));
+    if (steps_done) *steps_done = done;
+    return DNN_HIP_OK;
+}
+
+int engine_prefill(dnn_hip_session *s, const float *embeds, int n_embed, const int *ids, int n_ids_max,
+                   const int *n_ids, int mode, int prefix_len, int *next_ids, float *logits) {
+    dnn_hip_model *m = s->m;
+    const int B = s->B, D = m->D;
+    if (n_embed < 0 || n_ids_max < 0) return set_error(DNN_HIP_EINVAL, "n_embed %d / n_ids_max %d", n_embed, n_ids_max);
+    if (n_embed > 0 && !embeds) return set_error(DNN_HIP_EINVAL, "embeds is NULL");
+    if (mode != 0 && mode != 1) return set_error(DNN_HIP_EINVAL, "mode %d: 0 (causal) or 1 (prefix-LM)", mode);
+    std::vector<int> nn(B), row0(B), p0(B), arow(B);
+    int M = 0;
+    for (int b = 0; b < B; b++) {
+        const int ni = n_ids ? n_ids[b] : n_ids_max;
+        if (ni < 0 || ni > n_ids_max) return set_error(DNN_HIP_EINVAL, "row %d: %d ids of at most %d", b, ni, n_ids_max);
+        if (ni > 0 && !ids) return set_error(DNN_HIP_EINVAL, "ids is NULL");
+        for (int t = 0; t < ni; t++) {
+            const int id = ids[(size_t)b * n_ids_max + t];
+            if (id < 0 || id >= m->V) return set_error(DNN_HIP_ERANGE, "token id %d at row %d position %d outside [0,%d)", id, b, t, m->V);
+        }
+        nn[b] = n_embed + ni;
+        if (nn[b] < 1) return set_error(DNN_HIP_EINVAL, "row %d: no new rows", b);
+        p0[b] = s->h_pos[b];
+        if (mode == 1 && p0[b] != 0) return set_error(DNN_HIP_EINVAL, "prefix-LM prefill needs an empty cache (row %d holds %d)", b, p0[b]);
+        if (p0[b] + nn[b] > s->max_seq)
+            return set_error(DNN_HIP_ERANGE, "row %d: %d cached + %d new exceeds max_seq %d", b, p0[b], nn[b], s->max_seq);
+        if (m->rope && p0[b] + nn[b] > m->rope_rows)
+            return set_error(DNN_HIP_ERANGE, "row %d: position %d beyond the RoPE table (%d rows)", b, p0[b] + nn[b] - 1, m->rope_rows);
+        row0[b] = M;
+        arow[b] = M + nn[b] - 1;
+        M += nn[b];
+    }
+    HIP_TRY(hipSetDevice(m->device));
+    int rc = engine_get(s, M);
+    if (rc) return rc;
+    BatchEngine *e = s->eng;
+    // the plan: row_b, row_p, pid [M]; row0, n_new, p0, arow [B]; tiles [T][2]
+    std::vector<int> tiles;
+    for (int b = 0; b < B; b++)
+        for (int t0 = 0; t0 < nn[b]; t0 += 64) { tiles.push_back(b); tiles.push_back(t0); }
+    const int T = (int)tiles.size() / 2;
+    std::vector<int> plan((size_t)3 * M + 4 * B + tiles.size());
+    int *row_b = plan.data(), *row_p = row_b + M, *pid = row_p + M, *hrow0 = pid + M, *hnn = hrow0 + B,
+        *hp0 = hnn + B, *harow = hp0 + B, *htiles = harow + B;
+    for (int b = 0; b < B; b++) {
+        const int ni = nn[b] - n_embed;
+        for (int t = 0; t < nn[b]; t++) {
+            const int r = row0[b] + t;
+            row_b[r] = b;
+            row_p[r] = p0[b] + t;
+            pid[r] = t < n_embed ? -1 : ids[(size_t)b * n_ids_max + (t - n_embed)];
+        }
+        (void)ni;
+        hrow0[b] = row0[b]; hnn[b] = nn[b]; hp0[b] = p0[b]; harow[b] = arow[b];
+    }
+    std::copy(tiles.begin(), tiles.end(), htiles);
+    rc = grow(&e->pre_i, &e->pre_cap, plan.size());
+    if (rc) return rc;
+    HIP_TRY(hipMemcpyAsync(e->pre_i, plan.data(), plan.size() * sizeof(int), hipMemcpyHostToDevice, s->stream));
+    int *d = e->pre_i;
+    PrefillPlan pp{M, d, d + M, d + 2 * M, d + 3 * M, d + 3 * M + B, d + 3 * M + 2 * B, d + 3 * M + 3 * B,
+                   d + 3 * M + 4 * B, T, mode, prefix_len};
+    // embedding inputs (e.g. image patches) straight into their rows, token rows gathered
+    if (n_embed > 0)
+        for (int b = 0; b < B; b++)
+            HIP_TRY(hipMemcpy2DAsync(e->X + (size_t)row0[b] * m->ldD, (size_t)m->ldD * 4, embeds + (size_t)b * n_embed * D,
+                                     (size_t)D * 4, (size_t)D * 4, n_embed, hipMemcpyHostToDevice, s->stream));
+    EmbedArgs ea{};
+    ea.embed = reinterpret_cast<const float *>(m->arena) + m->off.embed / 4;
+    ea.ids = pp.pid; ea.out = e->X; ea.M = M; ea.ld = m->ldD; ea.D = D;
+    HIP_TRY(launch_embed(ea, s->stream));
+    HIP_TRY(hipEventRecord(s->ev0, s->stream));
+    for (int l = 0; l < m->L; l++) {
+        rc = enqueue_layer(s, l, &pp);
+        if (rc) return rc;
+    }
+    rc = enqueue_head(s, &pp, logits ? e->pre_logits : nullptr, e->next_ids, -1);
+    if (rc) return rc;
+    HIP_TRY(hipEventRecord(s->ev1, s->stream));
+    HIP_TRY(hipEventSynchronize(s->ev1));
+    HIP_TRY(hipEventElapsedTime(&s->last_ms, s->ev0, s->ev1));
+    HIP_TRY(hipMemcpy(next_ids, e->next_ids, sizeof(int) * B, hipMemcpyDeviceToHost));
+    if (logits) HIP_TRY(hipMemcpy(logits, e->pre_logits, sizeof(float) * (size_t)B * m->V, hipMemcpyDeviceToHost));
+    for (int b = 0; b < B; b++) s->h_pos[b] = p0[b] + nn[b];
+    HIP_TRY(hipMemcpy(s->pos, s->h_pos.data(), sizeof(int) * B, hipMemcpyHostToDevice));
+    return DNN_HIP_OK;
+}
+
+}  // namespace dnnhip

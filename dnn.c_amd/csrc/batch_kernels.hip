@@ -1,0 +1,723 @@
+// batch_kernels.hip -- kernels of the batched engine (gfx950, wave64).
+//
+// One decode step of M rows (or one multi-token prefill) is a chain of
+// kernels per layer, the transformer block of the reference
+// (transformer_block_forward_cached_ex, transformer.c:211-416) restated for
+// many rows at once:
+//
+//   gemm<EPI_QKV>    rms_norm (norm.c:404-495) -> qkv_proj (nn.c:27-36,
+//                    ops_matrix.c:1143-1151) -> split heads (multihead.c:240-263)
+//                    -> RoPE (rope.c:20-35) -> Q rows and the K/V cache rows at
+//                    each row's position (transformer.c:240-250, kv_cache_append)
+//   attn / prefill_attn   scores * 1/sqrt(d_k), causal or prefix-LM mask,
+//                    softmax, P.V (transformer.c:256-397)
+//   gemm<EPI_RES>    out_proj + bias + residual (ops_elem.c:122-128)
+//   gemm<EPI_SWIGLU> rms_norm -> gate/up + biases -> (g/(1+expf(-g)))*u
+//                    (nn.c:61-78, simd.h:394-397)
+//   gemm<EPI_RES>    down_proj + bias + residual
+//
+// and per step gemm<EPI_HEAD>: final rms_norm -> tied lm_head + bias
+// (gpt.c:117-122, ops_matrix.c:1124-1132) -> argmax, first index of the maximum
+// (gpt.c:220-230), whose last workgroup feeds the next step.
+//
+// GEMM: C[m][n] = sum_k A[m][k] W[n][k] on v_mfma_f32_16x16x4_f32.  Lane l of a
+// wavefront holds A[m0 + l%16][k0 + 4(l/16) + j] and W[n0 + l%16][k0 + 4(l/16) + j]
+// for j = 0..3 (one 16-byte load each: four MFMAs per 16-column k-step, the
+// k values of MFMA j interleaved by 4), and C[m0 + 4(l/16) + v][n0 + l%16] in
+// accumulator register v.  The rms_norm is folded in: the k-loop multiplies A
+// by gamma and accumulates sum(x^2) from the same registers, and the epilogue
+// scales the row by 1/sqrtf(sum(x^2)/d + eps) -- the reference's (x*rs)*gamma
+// product reassociated, a rounding-level difference covered by the logit
+// tolerance.
+//
+// Two GEMM shapes: decode (all M <= 64 rows in one tile, 16 columns per
+// workgroup, its four wavefronts splitting K; optionally split K over several
+// workgroups whose tagged partials the last one to arrive sums in a fixed
+// order), and prefill (128 x 128 tiles, a 64 x 64 block per wavefront).
+
+#include "batch.h"
+#include "decode_device.h"
+
+namespace dnnhip {
+
+namespace {
+
+constexpr int NTHR = 256;
+
+__device__ __forceinline__ f4 mfma4(float a, float b, f4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
+}
+
+// Four consecutive weights of one row as fp32: a 16-byte load (fp32) or an
+// 8-byte load of bf16 values widened exactly (bf16 is the top half of fp32).
+template <bool BF>
+__device__ __forceinline__ f4 ldw4(rsrc_t r, unsigned off_elems) {
+    if constexpr (BF) {
+        const u2 v = __builtin_bit_cast(u2, __builtin_amdgcn_raw_buffer_load_b64(r, off_elems * 2u, 0, CP_NT));
+        f4 o;
+        o.x = as_float(v.x << 16);
+        o.y = as_float(v.x & 0xffff0000u);
+        o.z = as_float(v.y << 16);
+        o.w = as_float(v.y & 0xffff0000u);
+        return o;
+    } else {
+        return __builtin_bit_cast(f4, __builtin_amdgcn_raw_buffer_load_b128(r, off_elems * 4u, 0, CP_NT));
+    }
+}
+
+__device__ __forceinline__ f4 lda4(rsrc_t r, unsigned off_bytes) {
+    return __builtin_bit_cast(f4, __builtin_amdgcn_raw_buffer_load_b128(r, off_bytes, 0, 0));
+}
+
+__device__ __forceinline__ void st_pair2(rsrc_t r, size_t pair, float v0, float v1, unsigned tag) {
+    const u4 w = {as_uint(v0), tag, as_uint(v1), tag};
+    __builtin_amdgcn_raw_buffer_store_b128(w, r, (unsigned)(pair * 8), 0, CP_SC1);
+}
+__device__ __forceinline__ u4 ld_pair2(rsrc_t r, size_t pair) {
+    return __builtin_bit_cast(u4, __builtin_amdgcn_raw_buffer_load_b128(r, (unsigned)(pair * 8), 0, CP_SC1));
+}
+
+// vmcnt(0): this wavefront's loads and stores are complete
+__device__ __forceinline__ void wait_stores() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
+
+// Arrive at a last-arriver counter after this workgroup's stores are complete;
+// true in every thread of the workgroup that arrived last (which resets it).
+__device__ __forceinline__ bool arrive_last(unsigned *cnt, unsigned n, int *s_flag) {
+    wait_stores();
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        const unsigned old = __hip_atomic_fetch_add(cnt, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        const bool last = old == n - 1;
+        if (last) __hip_atomic_store(cnt, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        *s_flag = last;
+    }
+    __syncthreads();
+    return *s_flag != 0;
+}
+
+// Kernel-entry view of the step state (all workgroups of a launch read the same
+// values: only the last workgroup of the head kernel changes them, after every
+// other workgroup of that launch has arrived).
+__device__ __forceinline__ bool step_done(const StepState *st) {
+    return __builtin_nontemporal_load(&st->done) != 0;
+}
+
+}  // namespace
+
+// ---------------------------------------------------------------------------
+// GEMM.  MT x NT 16x16 tiles per wavefront, WM x WN wavefronts over the block
+// tile, KW wavefronts splitting K; MT*NT... WM*WN*KW == 4.
+template <int MT, int NT, int WM, int WN, int KW, bool BF, int EPI, bool NORM>
+__global__ __launch_bounds__(NTHR) void gemm_kernel(const GemmArgs g) {
+    static_assert(WM * WN * KW == 4, "four wavefronts");
+    constexpr int BM = 16 * MT * WM, BN = 16 * NT * WN;
+    constexpr int LDR = BN + 1;
+    constexpr int U = 4;                                   // k-steps per loop iteration
+    __shared__ float red[KW][BM][LDR];
+    __shared__ float ssl[KW][BM];
+    __shared__ int s_flag;
+    __shared__ unsigned s_tag;
+
+    if (step_done(g.st)) return;
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int kw = w % KW, wn = (w / KW) % WN, wm = w / (KW * WN);
+    const int tile_n = blockIdx.x / g.ks, ksi = blockIdx.x - tile_n * g.ks, tile_m = blockIdx.y;
+    const int ntn = (g.N + BN - 1) / BN;
+    const int r16 = lane & 15, q4 = lane >> 4;
+    if (tid == 0) s_tag = __builtin_nontemporal_load(&g.st->tag);
+
+    // this wavefront's k-steps (16 columns each)
+    const int nks = g.K / 16, parts = g.ks * KW, part = ksi * KW + kw;
+    const int kb0 = part * nks / parts, kb1 = (part + 1) * nks / parts;
+
+    const rsrc_t ra = buf(g.A, (size_t)g.mpad * g.lda * 4);
+    const rsrc_t rw = buf(g.W, g.w_bytes);
+    const rsrc_t rg = buf(g.gamma, NORM ? (size_t)g.K * 4 : 0);
+    unsigned aoff[MT], woff[NT];
+#pragma unroll
+    for (int mt = 0; mt < MT; mt++) {
+        const int m = tile_m * BM + wm * 16 * MT + 16 * mt + r16;
+        int pm = m;
+        if (g.arow) pm = g.arow[m < g.M ? m : 0];
+        aoff[mt] = (unsigned)(((size_t)pm * g.lda + 4 * q4) * 4);
+    }
+#pragma unroll
+    for (int nt = 0; nt < NT; nt++) {
+        const int n = tile_n * BN + wn * 16 * NT + 16 * nt + r16;
+        woff[nt] = (unsigned)((size_t)n * g.ldw + 4 * q4);     // elements
+    }
+
+    f4 acc[MT][NT];
+#pragma unroll
+    for (int mt = 0; mt < MT; mt++)
+#pragma unroll
+        for (int nt = 0; nt < NT; nt++) acc[mt][nt] = f4{0.f, 0.f, 0.f, 0.f};
+    float ss[MT];
+#pragma unroll
+    for (int mt = 0; mt < MT; mt++) ss[mt] = 0.f;
+
+    for (int kb = kb0; kb < kb1; kb += U) {
+        f4 a[U][MT], b[U][NT], gm[U];
+#pragma unroll
+        for (int u = 0; u < U; u++) {
+#pragma unroll
+            for (int nt = 0; nt < NT; nt++) b[u][nt] = ldw4<BF>(rw, woff[nt] + (unsigned)((kb + u) * 16));
+#pragma unroll
+            for (int mt = 0; mt < MT; mt++) a[u][mt] = lda4(ra, aoff[mt] + (unsigned)((kb + u) * 64));
+            if (NORM) gm[u] = lda4(rg, (unsigned)(((kb + u) * 16 + 4 * q4) * 4));
+        }
+#pragma unroll
+        for (int u = 0; u < U; u++) {
+            if (NORM) {
+#pragma unroll
+                for (int mt = 0; mt < MT; mt++) {
+                    f4 &x = a[u][mt];
+                    ss[mt] += x.x * x.x + x.y * x.y + x.z * x.z + x.w * x.w;
+                    x.x *= gm[u].x; x.y *= gm[u].y; x.z *= gm[u].z; x.w *= gm[u].w;
+                }
+            }
+#pragma unroll
+            for (int mt = 0; mt < MT; mt++)
+#pragma unroll
+                for (int nt = 0; nt < NT; nt++) {
+                    acc[mt][nt] = mfma4(a[u][mt].x, b[u][nt].x, acc[mt][nt]);
+                    acc[mt][nt] = mfma4(a[u][mt].y, b[u][nt].y, acc[mt][nt]);
+                    acc[mt][nt] = mfma4(a[u][mt].z, b[u][nt].z, acc[mt][nt]);
+                    acc[mt][nt] = mfma4(a[u][mt].w, b[u][nt].w, acc[mt][nt]);
+                }
+        }
+    }
+
+    // the wavefront's tiles -> LDS (one copy per K-splitting wavefront)
+#pragma unroll
+    for (int mt = 0; mt < MT; mt++)
+#pragma unroll
+        for (int nt = 0; nt < NT; nt++) {
+            const int r = wm * 16 * MT + 16 * mt + 4 * q4, c = wn * 16 * NT + 16 * nt + r16;
+            red[kw][r + 0][c] = acc[mt][nt].x;
+            red[kw][r + 1][c] = acc[mt][nt].y;
+            red[kw][r + 2][c] = acc[mt][nt].z;
+            red[kw][r + 3][c] = acc[mt][nt].w;
+        }
+    if (NORM) {
+#pragma unroll
+        for (int mt = 0; mt < MT; mt++) {
+            float s = ss[mt];
+            s += __shfl_xor(s, 16);
+            s += __shfl_xor(s, 32);
+            if (wn == 0 && q4 == 0) ssl[kw][wm * 16 * MT + 16 * mt + r16] = s;
+        }
+    }
+    __syncthreads();
+    const unsigned tag = s_tag * 128u + (unsigned)g.kslot;
+
+    // split K over workgroups: publish the partial tile, the last to arrive sums
+    // all partials in workgroup order (a fixed order: the result does not
+    // depend on which one arrives last)
+    const rsrc_t rp = buf(g.part, g.part ? (size_t)g.ks * g.M * g.N * 8 : 0);
+    if (g.ks > 1) {
+        for (int i = tid; i < BM * BN / 2; i += NTHR) {
+            const int m = i / (BN / 2), n = 2 * (i - m * (BN / 2));
+            const int gm_ = tile_m * BM + m, gn = tile_n * BN + n;
+            if (gm_ >= g.M || gn >= g.N) continue;
+            float v0 = 0.f, v1 = 0.f;
+#pragma unroll
+            for (int k = 0; k < KW; k++) { v0 += red[k][m][n]; v1 += red[k][m][n + 1]; }
+            st_pair2(rp, ((size_t)ksi * g.M + gm_) * g.N + gn, v0, v1, tag);
+        }
+        if (!arrive_last(g.cnt + tile_n, (unsigned)g.ks, &s_flag)) return;
+    }
+
+    // epilogue: two adjacent columns per thread
+    for (int i = tid; i < BM * BN / 2; i += NTHR) {
+        const int m = i / (BN / 2), n = 2 * (i - m * (BN / 2));
+        const int gm_ = tile_m * BM + m, gn = tile_n * BN + n;
+        if (gm_ >= g.M || gn >= g.N) continue;
+        float v0 = 0.f, v1 = 0.f;
+        if (g.ks > 1) {
+            for (int k = 0; k < g.ks; k++) {
+                u4 p = ld_pair2(rp, ((size_t)k * g.M + gm_) * g.N + gn);
+                for (unsigned spin = 0; (p.y != tag || p.w != tag) && spin < SPIN_CAP; spin++) {
+                    __builtin_amdgcn_s_sleep(1);
+                    p = ld_pair2(rp, ((size_t)k * g.M + gm_) * g.N + gn);
+                }
+                v0 += as_float(p.x);
+                v1 += as_float(p.z);
+            }
+        } else {
+#pragma unroll
+            for (int k = 0; k < KW; k++) { v0 += red[k][m][n]; v1 += red[k][m][n + 1]; }
+        }
+        if (NORM) {
+            float s = 0.f;
+#pragma unroll
+            for (int k = 0; k < KW; k++) s += ssl[k][m];
+            const float rs = 1.0f / sqrtf(s * (1.0f / (float)g.dnorm) + g.eps);
+            v0 *= rs;
+            v1 *= rs;
+        }
+        if (EPI == EPI_RES) {
+            const float y0 = v0 + g.bias[gn], y1 = v1 + g.bias[gn + 1];
+            const float *rr = g.res + (size_t)gm_ * g.ldr + gn;
+            float *o = g.out + (size_t)gm_ * g.ldo + gn;
+            o[0] = rr[0] + y0;
+            o[1] = rr[1] + y1;
+        } else if (EPI == EPI_SWIGLU) {
+            // rows 2f (gate) and 2f+1 (up) of the interleaved gate/up matrix
+            const int f = gn >> 1;
+            const float gt = v0 + g.bias[f], up = v1 + g.bias2[f];
+            g.out[(size_t)gm_ * g.ldo + f] = (gt / (1.0f + expf(-gt))) * up;
+        } else if (EPI == EPI_QKV) {
+            float y0 = v0 + g.bias[gn], y1 = v1 + g.bias[gn + 1];
+            const int sec = gn / g.D, c = gn - sec * g.D, h = c / BK_DK, d = c - h * BK_DK;
+            const int b = g.row_b[gm_], p = g.row_p[gm_];
+            if (sec < 2 && g.rope) {
+                const float cs = g.rope[(size_t)p * (BK_DK / 2) + d / 2];
+                const float sn = g.rope[(size_t)(g.rope_rows + p) * (BK_DK / 2) + d / 2];
+                const float e = y0, o = y1;
+                y0 = e * cs - o * sn;
+                y1 = e * sn + o * cs;
+            }
+            const size_t head = (((size_t)g.layer * g.B + b) * g.H + h) * (size_t)BK_DK * g.kv_s;
+            if (sec == 0) {
+                g.q[(size_t)gm_ * g.D + c] = y0;
+                g.q[(size_t)gm_ * g.D + c + 1] = y1;
+            } else if (sec == 1) {
+                g.kc[head + (size_t)d * g.kv_s + p] = y0;
+                g.kc[head + (size_t)(d + 1) * g.kv_s + p] = y1;
+            } else {
+                g.vc[head + (size_t)p * BK_DK + d] = y0;
+                g.vc[head + (size_t)p * BK_DK + d + 1] = y1;
+            }
+        } else {   // EPI_HEAD: logits into the LDS tile for the argmax pass
+            const float y0 = v0 + g.bias[gn], y1 = v1 + g.bias[gn + 1];
+            red[0][m][n] = y0;
+            red[0][m][n + 1] = y1;
+            if (g.logits) {
+                const size_t row = g.prefill ? (size_t)gm_ : (size_t)g.st->t * g.M + gm_;
+                g.logits[row * g.N + gn] = y0;
+                g.logits[row * g.N + gn + 1] = y1;
+            }
+        }
+    }
+    if (EPI != EPI_HEAD) return;
+
+    // ---- argmax of this tile's columns per row, then the last workgroup of
+    // the launch reduces the tiles and feeds the next step
+    __syncthreads();
+    const rsrc_t rx = buf(g.amax, (size_t)g.M * ntn * 8);
+    for (int m = tid; m < BM; m += NTHR) {
+        const int gm_ = tile_m * BM + m;
+        if (gm_ >= g.M) continue;
+        float best = -INFINITY;
+        int bi = tile_n * BN;
+        for (int n = 0; n < BN; n++) {
+            const int gn = tile_n * BN + n;
+            if (gn < g.N && red[0][m][n] > best) { best = red[0][m][n]; bi = gn; }
+        }
+        const u2 pr = {as_uint(best), (unsigned)bi | (s_tag << 16)};
+        __builtin_amdgcn_raw_buffer_store_b64(pr, rx, (unsigned)(((size_t)gm_ * ntn + tile_n) * 8), 0, CP_SC1);
+    }
+    if (!arrive_last(g.head_cnt, (unsigned)(ntn * gridDim.y), &s_flag)) return;
+
+    // ---- the last workgroup: one wavefront per row
+    const int t = g.prefill ? 0 : g.st->t;
+    const unsigned tag16 = s_tag & 0xffffu;
+    for (int m = w; m < g.M; m += NTHR / 64) {
+        float best = -INFINITY;
+        int bi = 0x7fffffff;
+        for (int tn = lane; tn < ntn; tn += 64) {
+            u2 p = __builtin_bit_cast(u2, __builtin_amdgcn_raw_buffer_load_b64(rx, (unsigned)(((size_t)m * ntn + tn) * 8), 0, CP_SC1));
+            for (unsigned spin = 0; (p.y >> 16) != tag16 && spin < SPIN_CAP; spin++) {
+                __builtin_amdgcn_s_sleep(1);
+                p = __builtin_bit_cast(u2, __builtin_amdgcn_raw_buffer_load_b64(rx, (unsigned)(((size_t)m * ntn + tn) * 8), 0, CP_SC1));
+            }
+            const float v = as_float(p.x);
+            const int idx = (int)(p.y & 0xffffu);
+            if (v > best || (v == best && idx < bi)) { best = v; bi = idx; }
+        }
+        // wavefront reduction: larger value, then lower index
+#pragma unroll
+        for (int o = 32; o >= 1; o >>= 1) {
+            const float ov = __shfl_xor(best, o);
+            const int oi = __shfl_xor(bi, o);
+            if (ov > best || (ov == best && oi < bi)) { best = ov; bi = oi; }
+        }
+        if (bi == 0x7fffffff) bi = 0;
+        const int tok = bi;
+        if (g.prefill) {
+            if (lane == 0) g.ids[m] = tok;
+            continue;
+        }
+        if (lane == 0) {
+            g.ids[(size_t)t * g.M + m] = tok;
+            if (g.eos >= 0 && t >= g.n_feed[m] - 1 && tok == g.eos) g.row_done[m] = 1;
+            g.pos[m] += 1;
+        }
+        const int nxt = (t + 1 < g.n_feed[m]) ? g.feed[(size_t)(t + 1) * g.M + m] : tok;
+        const float *e = g.embed + (size_t)nxt * g.ldx;
+        float *x = g.x_next + (size_t)m * g.ldx;
+        for (int c = lane; c < g.D; c += 64) x[c] = e[c];
+    }
+    __syncthreads();
+    if (tid == 0) {
+        if (!g.prefill) {
+            int all = g.eos >= 0;
+            for (int m = 0; m < g.M; m++) all &= g.row_done[m];
+            g.st->t = t + 1;
+            *g.steps_done = t + 1;
+            if (all) g.st->done = 1;
+        }
+        g.st->tag = s_tag + 1;
+    }
+}
+
+// ---------------------------------------------------------------------------
+// Decode attention.  Workgroup (row m, head h, split s) takes the 64-key chunks
+// c = s (mod nsplit) of the row's S = pos[m] + 1 cached keys; wavefront w the
+// chunks with c / nsplit = w (mod 4).  Lane l holds keys 64c + 4(l%16) + 0..3
+// for the scores (dims l/16 + 4i from K^T, summed over the four lane groups),
+// and dims 4(l%16) + 0..3 of keys 64c + l/16 + 4i for P.V.  Running max /
+// sum per wavefront (transformer.c:354-359), merged across wavefronts in LDS
+// and across splits by the last workgroup of the (row, head).
+__global__ __launch_bounds__(NTHR) void attn_kernel(const AttnArgs a) {
+    __shared__ float s_p[4][64];
+    __shared__ float s_o[4][BK_DK];
+    __shared__ float s_ml[4][2];
+    __shared__ int s_flag;
+    __shared__ unsigned s_tag;
+    if (step_done(a.st)) return;
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int bh = blockIdx.x / a.nsplit, sp = blockIdx.x - bh * a.nsplit;
+    const int m = bh / a.H, h = bh - m * a.H;
+    if (tid == 0) s_tag = __builtin_nontemporal_load(&a.st->tag);
+    const int S = a.pos[m] + 1;
+    const int nch = (S + 63) / 64;
+    const int r16 = lane & 15, q4 = lane >> 4;
+    const size_t head = (((size_t)a.layer * a.B + m) * a.H + h) * (size_t)BK_DK * a.kv_s;
+    const rsrc_t rk = buf(a.kc + head, (size_t)BK_DK * a.kv_s * 4);
+    const rsrc_t rv = buf(a.vc + head, (size_t)BK_DK * a.kv_s * 4);
+    float qv[16];
+#pragma unroll
+    for (int i = 0; i < 16; i++) qv[i] = a.q[(size_t)m * a.D + h * BK_DK + q4 + 4 * i];
+
+    float mrun = -INFINITY, lrun = 0.f;
+    f4 o = {0.f, 0.f, 0.f, 0.f};
+    for (int c = sp + a.nsplit * w; c < nch; c += 4 * a.nsplit) {
+        const int j0 = 64 * c;
+        // scores of keys j0 + 4 r16 + 0..3
+        f4 kt[16];
+#pragma unroll
+        for (int i = 0; i < 16; i++)
+            kt[i] = lda4(rk, (unsigned)((((size_t)(q4 + 4 * i)) * a.kv_s + j0 + 4 * r16) * 4));
+        f4 vv[16];
+#pragma unroll
+        for (int i = 0; i < 16; i++)
+            vv[i] = lda4(rv, (unsigned)((((size_t)(j0 + q4 + 4 * i)) * BK_DK + 4 * r16) * 4));
+        f4 s = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int i = 0; i < 16; i++) {
+            s.x += qv[i] * kt[i].x; s.y += qv[i] * kt[i].y; s.z += qv[i] * kt[i].z; s.w += qv[i] * kt[i].w;
+        }
+#pragma unroll
+        for (int o2 = 16; o2 <= 32; o2 <<= 1) {
+            s.x += __shfl_xor(s.x, o2); s.y += __shfl_xor(s.y, o2);
+            s.z += __shfl_xor(s.z, o2); s.w += __shfl_xor(s.w, o2);
+        }
+        const int jb = j0 + 4 * r16;
+        s.x = jb + 0 < S ? s.x * 0.125f : -INFINITY;
+        s.y = jb + 1 < S ? s.y * 0.125f : -INFINITY;
+        s.z = jb + 2 < S ? s.z * 0.125f : -INFINITY;
+        s.w = jb + 3 < S ? s.w * 0.125f : -INFINITY;
+        float cm = fmaxf(fmaxf(s.x, s.y), fmaxf(s.z, s.w));
+#pragma unroll
+        for (int o2 = 1; o2 < 16; o2 <<= 1) cm = fmaxf(cm, __shfl_xor(cm, o2));
+        const float mnew = fmaxf(mrun, cm);
+        const float sc = expf(mrun - mnew);
+        f4 p;
+        p.x = expf(s.x - mnew); p.y = expf(s.y - mnew); p.z = expf(s.z - mnew); p.w = expf(s.w - mnew);
+        float ps = (p.x + p.y) + (p.z + p.w);
+#pragma unroll
+        for (int o2 = 1; o2 < 16; o2 <<= 1) ps += __shfl_xor(ps, o2);
+        lrun = lrun * sc + ps;
+        mrun = mnew;
+        if (q4 == 0) *reinterpret_cast<f4 *>(&s_p[w][4 * r16]) = p;
+        __builtin_amdgcn_s_waitcnt(0xc07f);
+        __builtin_amdgcn_wave_barrier();
+        o.x *= sc; o.y *= sc; o.z *= sc; o.w *= sc;
+#pragma unroll
+        for (int i = 0; i < 16; i++) {
+            const float pj = s_p[w][q4 + 4 * i];
+            o.x += pj * vv[i].x; o.y += pj * vv[i].y; o.z += pj * vv[i].z; o.w += pj * vv[i].w;
+        }
+        __builtin_amdgcn_wave_barrier();
+    }
+#pragma unroll
+    for (int o2 = 16; o2 <= 32; o2 <<= 1) {
+        o.x += __shfl_xor(o.x, o2); o.y += __shfl_xor(o.y, o2);
+        o.z += __shfl_xor(o.z, o2); o.w += __shfl_xor(o.w, o2);
+    }
+    if (q4 == 0) *reinterpret_cast<f4 *>(&s_o[w][4 * r16]) = o;
+    if (lane == 0) { s_ml[w][0] = mrun; s_ml[w][1] = lrun; }
+    __syncthreads();
+    // merge the four wavefronts: thread d < 64 owns output dim d
+    float om = -INFINITY;
+    for (int k = 0; k < 4; k++) om = fmaxf(om, s_ml[k][0]);
+    float ol = 0.f, od = 0.f;
+    if (tid < BK_DK) {
+        for (int k = 0; k < 4; k++) {
+            if (s_ml[k][0] == -INFINITY) continue;
+            const float f = expf(s_ml[k][0] - om);
+            ol += s_ml[k][1] * f;
+            od += s_o[k][tid] * f;
+        }
+    }
+    if (a.nsplit == 1) {
+        if (tid < BK_DK) a.att[(size_t)m * a.ldatt + h * BK_DK + tid] = od / ol;
+        return;
+    }
+    // publish (o, m, l) of this split as tagged pairs; the last split of the
+    // (row, head) to arrive merges all of them in split order
+    const unsigned tag = s_tag * 128u + (unsigned)a.kslot;
+    const size_t rec = (size_t)bh * a.nsplit + sp;
+    const rsrc_t rp = buf(a.part, (size_t)a.M * a.H * a.nsplit * (BK_DK + 2) * 8);
+    if (tid < BK_DK) put(rp, rec * (BK_DK + 2) + tid, od, tag);
+    if (tid == 0) { put(rp, rec * (BK_DK + 2) + BK_DK, om, tag); put(rp, rec * (BK_DK + 2) + BK_DK + 1, ol, tag); }
+    if (!arrive_last(a.cnt + bh, (unsigned)a.nsplit, &s_flag)) return;
+    if (tid >= BK_DK) return;
+    auto get = [&](size_t pr) {
+        u2 v = __builtin_bit_cast(u2, __builtin_amdgcn_raw_buffer_load_b64(rp, (unsigned)(pr * 8), 0, CP_SC1));
+        for (unsigned spin = 0; v.y != tag && spin < SPIN_CAP; spin++) {
+            __builtin_amdgcn_s_sleep(1);
+            v = __builtin_bit_cast(u2, __builtin_amdgcn_raw_buffer_load_b64(rp, (unsigned)(pr * 8), 0, CP_SC1));
+        }
+        return as_float(v.x);
+    };
+    float gm = -INFINITY;
+    for (int k = 0; k < a.nsplit; k++) gm = fmaxf(gm, get(((size_t)bh * a.nsplit + k) * (BK_DK + 2) + BK_DK));
+    float gl = 0.f, gd = 0.f;
+    for (int k = 0; k < a.nsplit; k++) {
+        const size_t r = ((size_t)bh * a.nsplit + k) * (BK_DK + 2);
+        const float km = get(r + BK_DK);
+        if (km == -INFINITY) continue;
+        const float f = expf(km - gm);
+        gl += get(r + BK_DK + 1) * f;
+        gd += get(r + tid) * f;
+    }
+    a.att[(size_t)m * a.ldatt + h * BK_DK + tid] = gd / gl;
+}
+
+// ---------------------------------------------------------------------------
+// Prefill attention (the multi-token cached forward, transformer.c:256-397,
+// and the full-sequence triangular form, attention.c:259-380).  Workgroup
+// (64-row tile of one sequence's new rows, head h); wavefront w owns rows
+// 16w .. 16w+15 of the tile.  Per 64-key tile: K^T and V staged in LDS,
+// S = Q K^T on MFMA (A: Q rows from registers, B: K^T from LDS), the causal /
+// prefix-LM mask (transformer.c:305-325: a row at position p sees keys
+// j < (p < prefix_len ? prefix_len : p + 1) in prefix-LM mode, j <= p
+// otherwise), running max / sum per row, P through LDS into the A layout, and
+// O += P V on MFMA.
+__global__ __launch_bounds__(NTHR) void prefill_attn_kernel(const PrefillAttnArgs a) {
+    __shared__ float Ks[BK_DK][65];
+    __shared__ float Vs[64][BK_DK + 1];
+    __shared__ float Ps[4][16][65];
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int r16 = lane & 15, q4 = lane >> 4;
+    const int tile = blockIdx.x, h = blockIdx.y;
+    const int b = a.tiles[2 * tile], t0 = a.tiles[2 * tile + 1];
+    const int nn = a.n_new[b], p0 = a.p0[b], r0 = a.row0[b];
+    const int nq = min(64, nn - t0);
+    int kv_end = p0 + t0 + nq;
+    if (a.mode == 1 && kv_end < a.prefix_len) kv_end = a.prefix_len;
+    kv_end = min(kv_end, p0 + nn);
+    const size_t head = (((size_t)a.layer * a.B + b) * a.H + h) * (size_t)BK_DK * a.kv_s;
+    const rsrc_t rk = buf(a.kc + head, (size_t)BK_DK * a.kv_s * 4);
+    const rsrc_t rv = buf(a.vc + head, (size_t)BK_DK * a.kv_s * 4);
+
+    // Q fragments of row 16w + r16 (clamped into the tile), dims 16s + 4 q4 + j
+    const int qi = min(16 * w + r16, nq - 1);
+    const float *qrow = a.q + (size_t)(r0 + t0 + qi) * a.D + h * BK_DK;
+    f4 qf[4];
+#pragma unroll
+    for (int s = 0; s < 4; s++) qf[s] = *reinterpret_cast<const f4 *>(qrow + 16 * s + 4 * q4);
+    // visible keys of the accumulator rows 16w + 4 q4 + v
+    int vis[4];
+#pragma unroll
+    for (int v = 0; v < 4; v++) {
+        const int p = p0 + t0 + 16 * w + 4 * q4 + v;
+        vis[v] = (a.mode == 1 && p < a.prefix_len) ? a.prefix_len : p + 1;
+    }
+    float mr[4], lr[4];
+    f4 O[4];
+#pragma unroll
+    for (int v = 0; v < 4; v++) { mr[v] = -INFINITY; lr[v] = 0.f; O[v] = f4{0.f, 0.f, 0.f, 0.f}; }
+
+    for (int key0 = 0; key0 < kv_end; key0 += 64) {
+        __syncthreads();
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const int rr = tid / 16 + 16 * i, cc = 4 * (tid % 16);
+            const f4 kv = lda4(rk, (unsigned)(((size_t)rr * a.kv_s + key0 + cc) * 4));
+            Ks[rr][cc] = kv.x; Ks[rr][cc + 1] = kv.y; Ks[rr][cc + 2] = kv.z; Ks[rr][cc + 3] = kv.w;
+            const f4 vv = lda4(rv, (unsigned)(((size_t)(key0 + rr) * BK_DK + cc) * 4));
+            Vs[rr][cc] = vv.x; Vs[rr][cc + 1] = vv.y; Vs[rr][cc + 2] = vv.z; Vs[rr][cc + 3] = vv.w;
+        }
+        __syncthreads();
+        f4 S[4];
+#pragma unroll
+        for (int nt = 0; nt < 4; nt++) S[nt] = f4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int s = 0; s < 4; s++)
+#pragma unroll
+            for (int j = 0; j < 4; j++) {
+                const float av = qf[s][j];
+#pragma unroll
+                for (int nt = 0; nt < 4; nt++) S[nt] = mfma4(av, Ks[16 * s + 4 * q4 + j][16 * nt + r16], S[nt]);
+            }
+        float sc[4];
+#pragma unroll
+        for (int v = 0; v < 4; v++) {
+            float mx = -INFINITY;
+#pragma unroll
+            for (int nt = 0; nt < 4; nt++) {
+                const int key = key0 + 16 * nt + r16;
+                const float x = key < vis[v] ? S[nt][v] * 0.125f : -INFINITY;
+                S[nt][v] = x;
+                mx = fmaxf(mx, x);
+            }
+#pragma unroll
+            for (int o2 = 1; o2 < 16; o2 <<= 1) mx = fmaxf(mx, __shfl_xor(mx, o2));
+            const float mnew = fmaxf(mr[v], mx);
+            const float base = mnew == -INFINITY ? 0.f : mnew;
+            sc[v] = expf(mr[v] - base);
+            float ps = 0.f;
+#pragma unroll
+            for (int nt = 0; nt < 4; nt++) {
+                const float x = expf(S[nt][v] - base);
+                S[nt][v] = x;
+                ps += x;
+            }
+#pragma unroll
+            for (int o2 = 1; o2 < 16; o2 <<= 1) ps += __shfl_xor(ps, o2);
+            lr[v] = lr[v] * sc[v] + ps;
+            mr[v] = mnew;
+        }
+#pragma unroll
+        for (int nt = 0; nt < 4; nt++) {
+            Ps[w][4 * q4 + 0][16 * nt + r16] = S[nt].x;
+            Ps[w][4 * q4 + 1][16 * nt + r16] = S[nt].y;
+            Ps[w][4 * q4 + 2][16 * nt + r16] = S[nt].z;
+            Ps[w][4 * q4 + 3][16 * nt + r16] = S[nt].w;
+            O[nt].x *= sc[0]; O[nt].y *= sc[1]; O[nt].z *= sc[2]; O[nt].w *= sc[3];
+        }
+        __builtin_amdgcn_s_waitcnt(0xc07f);
+        __builtin_amdgcn_wave_barrier();
+#pragma unroll
+        for (int s = 0; s < 4; s++)
+#pragma unroll
+            for (int j = 0; j < 4; j++) {
+                const float pv = Ps[w][r16][16 * s + 4 * q4 + j];
+#pragma unroll
+                for (int nt = 0; nt < 4; nt++) O[nt] = mfma4(pv, Vs[16 * s + 4 * q4 + j][16 * nt + r16], O[nt]);
+            }
+        __builtin_amdgcn_wave_barrier();
+    }
+#pragma unroll
+    for (int v = 0; v < 4; v++) {
+        const int i = 16 * w + 4 * q4 + v;
+        if (i >= nq) continue;
+        float *o = a.att + (size_t)(r0 + t0 + i) * a.ldatt + h * BK_DK;
+        const float inv = lr[v];
+#pragma unroll
+        for (int nt = 0; nt < 4; nt++) {
+            o[16 * nt + r16] = O[nt][v] / inv;
+        }
+    }
+}
+
+// ---------------------------------------------------------------------------
+// Embedding rows (embedding.c:79-84) and the reset of the step counters of a
+// decode call.
+__global__ __launch_bounds__(NTHR) void embed_kernel(const EmbedArgs a) {
+    const int m = blockIdx.x;
+    if (m == 0 && threadIdx.x == 0 && a.st) { a.st->t = 0; a.st->done = 0; }
+    if (threadIdx.x == 0 && a.row_done) a.row_done[m] = 0;
+    const int id = a.ids[m];
+    if (id < 0) return;
+    const float *e = a.embed + (size_t)id * a.ld;
+    float *x = a.out + (size_t)m * a.ld;
+    for (int c = threadIdx.x; c < a.D; c += NTHR) x[c] = e[c];
+}
+
+// ---------------------------------------------------------------------------
+// launchers
+
+namespace {
+
+template <int EPI, bool NORM, bool BF>
+hipError_t gemm_decode(const GemmArgs &g, hipStream_t st) {
+    const int ntn = (g.N + 15) / 16;
+    dim3 grid(ntn * g.ks, 1);
+    const int mt = (g.M + 15) / 16;
+    switch (mt) {
+        case 1: hipLaunchKernelGGL((gemm_kernel<1, 1, 1, 1, 4, BF, EPI, NORM>), grid, dim3(NTHR), 0, st, g); break;
+        case 2: hipLaunchKernelGGL((gemm_kernel<2, 1, 1, 1, 4, BF, EPI, NORM>), grid, dim3(NTHR), 0, st, g); break;
+        case 3: hipLaunchKernelGGL((gemm_kernel<3, 1, 1, 1, 4, BF, EPI, NORM>), grid, dim3(NTHR), 0, st, g); break;
+        default: hipLaunchKernelGGL((gemm_kernel<4, 1, 1, 1, 4, BF, EPI, NORM>), grid, dim3(NTHR), 0, st, g); break;
+    }
+    return hipGetLastError();
+}
+
+template <int EPI, bool NORM, bool BF>
+hipError_t gemm_prefill(const GemmArgs &g, hipStream_t st) {
+    dim3 grid((g.N + BK_PBN - 1) / BK_PBN * g.ks, (g.M + BK_PBM - 1) / BK_PBM);
+    hipLaunchKernelGGL((gemm_kernel<4, 4, 2, 2, 1, BF, EPI, NORM>), grid, dim3(NTHR), 0, st, g);
+    return hipGetLastError();
+}
+
+template <bool BF>
+hipError_t gemm_any(int epi, bool norm, bool prefill, const GemmArgs &g, hipStream_t st) {
+    if (prefill) {
+        switch (epi) {
+            case EPI_QKV: return norm ? gemm_prefill<EPI_QKV, true, BF>(g, st) : hipErrorInvalidValue;
+            case EPI_RES: return norm ? hipErrorInvalidValue : gemm_prefill<EPI_RES, false, BF>(g, st);
+            case EPI_SWIGLU: return norm ? gemm_prefill<EPI_SWIGLU, true, BF>(g, st) : hipErrorInvalidValue;
+            default: return hipErrorInvalidValue;
+        }
+    }
+    switch (epi) {
+        case EPI_QKV: return norm ? gemm_decode<EPI_QKV, true, BF>(g, st) : hipErrorInvalidValue;
+        case EPI_RES: return norm ? hipErrorInvalidValue : gemm_decode<EPI_RES, false, BF>(g, st);
+        case EPI_SWIGLU: return norm ? gemm_decode<EPI_SWIGLU, true, BF>(g, st) : hipErrorInvalidValue;
+        case EPI_HEAD: return norm ? gemm_decode<EPI_HEAD, true, BF>(g, st) : hipErrorInvalidValue;
+        default: return hipErrorInvalidValue;
+    }
+}
+
+}  // namespace
+
+hipError_t launch_gemm(int epi, bool norm, bool bf16, bool prefill, const GemmArgs &g, hipStream_t stream) {
+    return bf16 ? gemm_any<true>(epi, norm, prefill, g, stream) : gemm_any<false>(epi, norm, prefill, g, stream);
+}
+
+hipError_t launch_attn(const AttnArgs &a, hipStream_t stream) {
+    hipLaunchKernelGGL(attn_kernel, dim3(a.M * a.H * a.nsplit), dim3(NTHR), 0, stream, a);
+    return hipGetLastError();
+}
+
+hipError_t launch_prefill_attn(const PrefillAttnArgs &a, hipStream_t stream) {
+    hipLaunchKernelGGL(prefill_attn_kernel, dim3(a.n_tiles, a.H), dim3(NTHR), 0, stream, a);
+    return hipGetLastError();
+}
+
+hipError_t launch_embed(const EmbedArgs &a, hipStream_t stream) {
+    hipLaunchKernelGGL(embed_kernel, dim3(a.M), dim3(NTHR), 0, stream, a);
+    return hipGetLastError();
+}
+
+int gemm_tile_rows(bool prefill, int M) { return prefill ? BK_PBM : (M + 15) / 16 * 16; }
+
+}  // namespace dnnhip

@@ -12,7 +12,7 @@ constexpr int WPB = BLOCK / WAVE;
 constexpr int CH = 32;            // cached keys per attention work unit (two half-waves per key)
 constexpr int DK = 64;            // head dimension the kernels are built for
 constexpr int MAXB = 8;           // batch rows per decode launch
-constexpr int MAX_ROWS = 64;      // rows per session (groups of MAXB run in turn)
+constexpr int MAX_ROWS = 64;      // rows per session (more than MAXB: the batched engine)
 constexpr int LDALIGN = 256;      // weight rows / activation rows padded to this many floats
 constexpr int FCMAX = 8;          // down-projection input chunks of 256: d_ffn <= 2048
 
@@ -86,14 +86,6 @@ struct DecodeArgs {
     unsigned step0;         // tag of this launch's first step (>= 1, increasing)
     int *err;               // bit 0: a dependency wait hit its spin cap
     int *steps_done;
-};
-
-// Sessions decoded by one launch of the general kernel (groups of a session
-// of more than MAXB rows): session i on workgroups [i * per, (i + 1) * per).
-constexpr int MAX_GROUPS = MAX_ROWS / MAXB;
-struct MultiArgs {
-    DecodeArgs a[MAX_GROUPS];
-    int n, per;
 };
 
 // Dynamic LDS of the decode kernel (bytes): per-row token / position / done
@@ -193,7 +185,6 @@ struct StreamArgs {
 };
 
 const void *decode_kernel_for(int nb, int dc);
-const void *decode_multi_for(int dc);
 const void *decode_lookahead_for(int nb, int dc);
 const void *decode_stream_for(int nb, int dc);
 

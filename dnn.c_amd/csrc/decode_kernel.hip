@@ -501,32 +501,11 @@ decode_v3(DecodeArgs a) {
     decode_v3_body<NB, DC>(a, gridDim.x, blockIdx.x);
 }
 
-// Several sessions in one launch: session i runs on workgroups
-// [i * per, (i + 1) * per).  Persistent launches on separate streams are not
-// co-resident on this device, so a multi-session batch shares one grid.
-template <int NB, int DC>
-__global__ void __launch_bounds__(BLOCK)
-decode_v3_multi(MultiArgs m) {
-    const int i = blockIdx.x / m.per;
-    if (i >= m.n) return;
-    decode_v3_body<NB, DC>(m.a[i], m.per, blockIdx.x - i * m.per);
-}
-
 #define DNNHIP_INST(NB, DC) template __global__ void decode_v3<NB, DC>(DecodeArgs);
 DNNHIP_INST(1, 1) DNNHIP_INST(1, 2) DNNHIP_INST(1, 3)
 DNNHIP_INST(2, 1) DNNHIP_INST(2, 2) DNNHIP_INST(2, 3)
 DNNHIP_INST(4, 1) DNNHIP_INST(4, 2) DNNHIP_INST(4, 3)
 DNNHIP_INST(8, 1) DNNHIP_INST(8, 2) DNNHIP_INST(8, 3)
-
-template __global__ void decode_v3_multi<8, 1>(MultiArgs);
-template __global__ void decode_v3_multi<8, 2>(MultiArgs);
-template __global__ void decode_v3_multi<8, 3>(MultiArgs);
-const void *decode_multi_for(int dc) {
-    if (dc == 1) return reinterpret_cast<const void *>(&decode_v3_multi<8, 1>);
-    if (dc == 2) return reinterpret_cast<const void *>(&decode_v3_multi<8, 2>);
-    if (dc == 3) return reinterpret_cast<const void *>(&decode_v3_multi<8, 3>);
-    return nullptr;
-}
 
 const void *decode_kernel_for(int nb, int dc) {
 #define DNNHIP_PICK(NB, DC) if (nb == NB && dc == DC) return reinterpret_cast<const void *>(&decode_v3<NB, DC>);

@@ -11,6 +11,7 @@
 
 #include "../../include/dnn_hip.h"
 #include "decode_kernel.h"
+#include "session.h"
 
 using namespace dnnhip;
 
@@ -18,14 +19,9 @@ namespace {
 
 thread_local std::string g_err;
 
-int fail(int code, const char *fmt, ...) {
-    char buf[512];
-    va_list ap;
-    va_start(ap, fmt);
-    vsnprintf(buf, sizeof buf, fmt, ap);
-    va_end(ap);
-    g_err = buf;
-    return code;
+template <class... A>
+int fail(int code, const char *fmt, A... args) {
+    return dnnhip::set_error(code, fmt, args...);
 }
 
 #define HIP_TRY(expr)                                                                  \
@@ -39,44 +35,15 @@ inline size_t round_up(size_t v, size_t a) { return (v + a - 1) / a * a; }
 
 }  // namespace
 
-struct dnn_hip_model {
-    int V, D, L, H, dk, F, ldD, ldF;
-    int device;
-    char *arena = nullptr;
-    size_t arena_bytes = 0;
-    LayerOff *d_layers = nullptr;    // [L] float offsets of each block's tensors
-    float eps_final = 1e-5f;
-    std::vector<float> eps;          // 2L+1
-    float *rope = nullptr;           // [2][rope_rows][dk/2]: cos, then sin
-    int rope_rows = 0;
-    // byte offsets of every device tensor inside the arena, for the uploads
-    struct Off { size_t embed, lm_bias, g_final; std::vector<size_t> l; } off;
-};
-
-struct dnn_hip_session {
-    dnn_hip_model *m;
-    int B, max_seq;
-    hipStream_t stream = nullptr;
-    hipEvent_t ev0 = nullptr, ev1 = nullptr;
-    float *kc = nullptr, *vc = nullptr;       // K^T [L][B][H][DK][max_seq], V [L][B][H][max_seq][DK]
-    uint2 *xa = nullptr;                      // exchange arena (tagged pairs)
-    Exch ex{};
-    int *pos = nullptr, *steps_done = nullptr, *err = nullptr;
-    int *feed = nullptr, *n_feed = nullptr, *ids = nullptr;
-    size_t feed_cap = 0, ids_cap = 0;
-    float *logits = nullptr;
-    size_t logits_cap = 0;
-    int grid_req = 0, grid = 0, grid_cap = 0;
-    unsigned next_tag = 1;                    // tags only grow: stale values never match
-    int kernel_pref = 0;                      // env DNN_HIP_DECODE_KERNEL: 4 / 5: the lookahead / streaming kernel where it applies
-    int kernel_used = 0;                      // 3, 4 or 5: the kernel of the last launch
-    size_t xa_pairs = 0;
-    float last_ms = 0.f;
-    std::vector<int> h_pos;
-    // more than MAXB rows: consecutive groups of at most MAXB rows, each its own
-    // session, run one after another by dnn_hip_decode
-    std::vector<dnn_hip_session *> groups;
-};
+int dnnhip::set_error(int code, const char *fmt, ...) {
+    char buf[512];
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(buf, sizeof buf, fmt, ap);
+    va_end(ap);
+    g_err = buf;
+    return code;
+}
 
 namespace {
 
@@ -149,6 +116,32 @@ int upload(dnn_hip_model *m, const float *const *params, int n_params) {
         transpose_into(at(o[P_WD]), p[P_WD], F, D, ldF, 1);
         memcpy(at(o[P_BD]), p[P_BD], sizeof(float) * D);
     }
+    if (m->bf16) {
+        // W16A32: every weight matrix rounded to bf16 (round to nearest even);
+        // the fp32 arena keeps the rounded values too (the embedding gather and
+        // the persistent kernels read it), the bf16 arena feeds the batched GEMMs
+        std::vector<uint16_t> h16(m->arena_bytes / sizeof(float), 0);
+        auto round_range = [&](size_t off, size_t n) {
+            uint32_t *f = reinterpret_cast<uint32_t *>(host.data() + off);
+            uint16_t *h = h16.data() + off / sizeof(float);
+            for (size_t i = 0; i < n; i++) {
+                const uint32_t u = f[i];
+                const uint32_t r = (u + 0x7fffu + ((u >> 16) & 1u)) >> 16;
+                h[i] = (uint16_t)r;
+                f[i] = r << 16;
+            }
+        };
+        round_range(m->off.embed, (size_t)V * ldD);
+        for (int l = 0; l < m->L; l++) {
+            const size_t *o = &m->off.l[(size_t)l * NPL];
+            round_range(o[P_WQKV], (size_t)3 * D * ldD);
+            round_range(o[P_WO], (size_t)D * ldD);
+            round_range(o[P_WG], (size_t)2 * F * ldD);
+            round_range(o[P_WD], (size_t)D * ldF);
+        }
+        HIP_TRY(hipSetDevice(m->device));
+        HIP_TRY(hipMemcpy(m->arena16, h16.data(), h16.size() * sizeof(uint16_t), hipMemcpyHostToDevice));
+    }
     HIP_TRY(hipSetDevice(m->device));
     HIP_TRY(hipMemcpy(m->arena, host.data(), m->arena_bytes, hipMemcpyHostToDevice));
     return DNN_HIP_OK;
@@ -158,24 +151,6 @@ void free_session_buffers(dnn_hip_session *s) {
     void *bufs[] = {s->kc, s->vc, s->xa, s->pos, s->steps_done, s->err, s->feed, s->n_feed, s->ids, s->logits};
     for (void *p : bufs)
         if (p) (void)hipFree(p);
-}
-
-template <class T>
-int dalloc(T **p, size_t count) {
-    hipError_t e = hipMalloc(reinterpret_cast<void **>(p), std::max<size_t>(count, 1) * sizeof(T));
-    if (e != hipSuccess) { *p = nullptr; return fail(DNN_HIP_ENOMEM, "hipMalloc(%zu bytes): %s", count * sizeof(T), hipGetErrorString(e)); }
-    return DNN_HIP_OK;
-}
-
-template <class T>
-int grow(T **p, size_t *cap, size_t count) {
-    if (count <= *cap) return DNN_HIP_OK;
-    if (*p) (void)hipFree(*p);
-    *p = nullptr;
-    *cap = 0;
-    int rc = dalloc(p, count);
-    if (rc == DNN_HIP_OK) *cap = count;
-    return rc;
 }
 
 int pick_nb(int B) { return B > 4 ? 8 : B > 2 ? 4 : B > 1 ? 2 : 1; }
@@ -229,7 +204,14 @@ int dnn_hip_init(int device) {
 
 int dnn_hip_model_create(int V, int D, int L, int H, int dk, int F, const float *const *params,
                          int n_params, const float *eps, dnn_hip_model **out) {
+    return dnn_hip_model_create_ex(V, D, L, H, dk, F, params, n_params, eps, DNN_HIP_WEIGHTS_F32, out);
+}
+
+int dnn_hip_model_create_ex(int V, int D, int L, int H, int dk, int F, const float *const *params,
+                            int n_params, const float *eps, int weights, dnn_hip_model **out) {
     if (!out) return fail(DNN_HIP_EINVAL, "out is NULL");
+    if (weights != DNN_HIP_WEIGHTS_F32 && weights != DNN_HIP_WEIGHTS_BF16)
+        return fail(DNN_HIP_EINVAL, "weights %d: DNN_HIP_WEIGHTS_F32 or DNN_HIP_WEIGHTS_BF16", weights);
     *out = nullptr;
     if (V <= 0 || D <= 0 || L <= 0 || H <= 0 || F <= 0 || dk <= 0)
         return fail(DNN_HIP_EINVAL, "non-positive dimension");
@@ -245,6 +227,7 @@ int dnn_hip_model_create(int V, int D, int L, int H, int dk, int F, const float 
     m->ldD = (int)round_up(D, LDALIGN);
     m->ldF = (int)round_up(F, LDALIGN);
     m->device = dev;
+    m->bf16 = weights == DNN_HIP_WEIGHTS_BF16;
     m->eps.assign(2 * L + 1, 1e-5f);
     if (eps) for (int i = 0; i < 2 * L + 1; i++) m->eps[i] = eps[i];
     m->eps_final = m->eps[2 * L];
@@ -257,8 +240,16 @@ int dnn_hip_model_create(int V, int D, int L, int H, int dk, int F, const float 
     }
     hipError_t e = hipMalloc(reinterpret_cast<void **>(&m->arena), m->arena_bytes);
     if (e != hipSuccess) { delete m; return fail(DNN_HIP_ENOMEM, "hipMalloc(%zu) for weights: %s", m->arena_bytes, hipGetErrorString(e)); }
+    if (m->bf16) {
+        e = hipMalloc(reinterpret_cast<void **>(&m->arena16), m->arena_bytes / 2);
+        if (e != hipSuccess) {
+            (void)hipFree(m->arena);
+            delete m;
+            return fail(DNN_HIP_ENOMEM, "hipMalloc(%zu) for bf16 weights: %s", m->arena_bytes / 2, hipGetErrorString(e));
+        }
+    }
     int rc = upload(m, params, n_params);
-    if (rc != DNN_HIP_OK) { (void)hipFree(m->arena); delete m; return rc; }
+    if (rc != DNN_HIP_OK) { (void)hipFree(m->arena); if (m->arena16) (void)hipFree(m->arena16); delete m; return rc; }
     auto fo = [](size_t byte_off) { return (uint32_t)(byte_off / sizeof(float)); };
     std::vector<LayerOff> lo(L);
     for (int l = 0; l < L; l++) {
@@ -272,6 +263,7 @@ int dnn_hip_model_create(int V, int D, int L, int H, int dk, int F, const float 
         w.eps_attn = m->eps[2 * l];
         w.eps_ffn = m->eps[2 * l + 1];
     }
+    m->h_layers = lo;
     e = hipMalloc(reinterpret_cast<void **>(&m->d_layers), sizeof(LayerOff) * L);
     if (e == hipSuccess) e = hipMemcpy(m->d_layers, lo.data(), sizeof(LayerOff) * L, hipMemcpyHostToDevice);
     if (e != hipSuccess) {
@@ -309,6 +301,7 @@ int dnn_hip_model_destroy(dnn_hip_model *m) {
     if (!m) return DNN_HIP_OK;
     (void)hipSetDevice(m->device);
     if (m->arena) (void)hipFree(m->arena);
+    if (m->arena16) (void)hipFree(m->arena16);
     if (m->d_layers) (void)hipFree(m->d_layers);
     if (m->rope) (void)hipFree(m->rope);
     delete m;
@@ -321,35 +314,23 @@ int dnn_hip_session_create(dnn_hip_model *m, int B, int max_seq, dnn_hip_session
     if (B <= 0 || B > MAX_ROWS) return fail(DNN_HIP_EINVAL, "batch %d outside [1,%d]", B, MAX_ROWS);
     if (max_seq <= 0) return fail(DNN_HIP_EINVAL, "max_seq %d", max_seq);
     HIP_TRY(hipSetDevice(m->device));
-    if (B > MAXB) {
-        auto *s = new dnn_hip_session();
-        s->m = m;
-        s->B = B;
-        s->max_seq = max_seq;
-        for (int r0 = 0; r0 < B; r0 += MAXB) {
-            dnn_hip_session *g = nullptr;
-            const int rc = dnn_hip_session_create(m, std::min(MAXB, B - r0), max_seq, &g);
-            if (rc) { dnn_hip_session_destroy(s); return rc; }
-            s->groups.push_back(g);
-        }
-        *out = s;
-        return DNN_HIP_OK;
-    }
     auto *s = new dnn_hip_session();
     s->m = m;
     s->B = B;
     s->max_seq = max_seq;
+    s->kv_s = (int)round_up((size_t)max_seq, BK_SEQ_ALIGN);
     s->h_pos.assign(B, 0);
-    if (const char *k = getenv("DNN_HIP_DECODE_KERNEL")) s->kernel_pref = atoi(k);   // "4": lookahead kernel
+    if (const char *k = getenv("DNN_HIP_DECODE_KERNEL")) s->kernel_pref = atoi(k);
+    // more than MAXB rows, bf16 weights, or on request: the batched engine
+    s->batched = B > MAXB || m->bf16 || s->kernel_pref == 6;
     int n_cu = 0;
     if (hipDeviceGetAttribute(&n_cu, hipDeviceAttributeMultiprocessorCount, m->device) != hipSuccess || n_cu <= 0) n_cu = 256;
     s->grid_cap = n_cu;
     s->ex = Exch{m->ldD, m->ldF, m->D, B, s->grid_cap};
-    // + CH*DK floats of zeroed padding: attention reads whole 32-key chunks,
-    // and the rows past max_seq of the last head must stay inside the allocation
-    const size_t kv = (size_t)m->L * B * m->H * max_seq * DK + (size_t)CH * DK;
-    size_t xa_pairs = s->ex.total(m->L);
-    if (B <= 2) {
+    // the kernels read whole 64-key chunks: the row stride kv_s covers them
+    const size_t kv = (size_t)m->L * B * m->H * s->kv_s * DK + (size_t)CH * DK;
+    size_t xa_pairs = s->batched ? 1 : s->ex.total(m->L);
+    if (!s->batched && B <= 2) {
         // room for the streaming kernel's exchange layout (its grid <= grid_cap)
         const int nb = pick_nb(B);
         const Exch5 e5{m->D, m->F, B, m->H, stream_splits(nb), s->grid_cap};
@@ -390,11 +371,6 @@ int dnn_hip_session_create(dnn_hip_model *m, int B, int max_seq, dnn_hip_session
 
 int dnn_hip_session_reset(dnn_hip_session *s) {
     if (!s) return fail(DNN_HIP_EINVAL, "session is NULL");
-    for (dnn_hip_session *g : s->groups) {
-        const int rc = dnn_hip_session_reset(g);
-        if (rc) return rc;
-    }
-    if (!s->groups.empty()) return DNN_HIP_OK;
     HIP_TRY(hipSetDevice(s->m->device));
     HIP_TRY(hipMemset(s->pos, 0, sizeof(int) * (size_t)s->B));
     std::fill(s->h_pos.begin(), s->h_pos.end(), 0);
@@ -403,23 +379,15 @@ int dnn_hip_session_reset(dnn_hip_session *s) {
 
 int dnn_hip_session_lengths(dnn_hip_session *s, int *lens) {
     if (!s || !lens) return fail(DNN_HIP_EINVAL, "NULL argument");
-    if (!s->groups.empty()) {
-        int r0 = 0;
-        for (dnn_hip_session *g : s->groups) {
-            dnn_hip_session_lengths(g, lens + r0);
-            r0 += g->B;
-        }
-        return DNN_HIP_OK;
-    }
     memcpy(lens, s->h_pos.data(), sizeof(int) * (size_t)s->B);
     return DNN_HIP_OK;
 }
 
 int dnn_hip_session_destroy(dnn_hip_session *s) {
     if (!s) return DNN_HIP_OK;
-    for (dnn_hip_session *g : s->groups) dnn_hip_session_destroy(g);
     (void)hipSetDevice(s->m->device);
     if (s->stream) (void)hipStreamSynchronize(s->stream);
+    if (s->eng) engine_destroy(s->eng);
     free_session_buffers(s);
     if (s->ev0) (void)hipEventDestroy(s->ev0);
     if (s->ev1) (void)hipEventDestroy(s->ev1);
@@ -430,20 +398,19 @@ int dnn_hip_session_destroy(dnn_hip_session *s) {
 
 int dnn_hip_session_set_grid(dnn_hip_session *s, int n) {
     if (!s || n < 0) return fail(DNN_HIP_EINVAL, "bad argument");
-    for (dnn_hip_session *g : s->groups) g->grid_req = n;
     s->grid_req = n;
     return DNN_HIP_OK;
 }
 
 int dnn_hip_session_grid(dnn_hip_session *s, int *grid) {
     if (!s || !grid) return fail(DNN_HIP_EINVAL, "NULL argument");
-    *grid = s->groups.empty() ? s->grid : s->groups[0]->grid;
+    *grid = s->grid;
     return DNN_HIP_OK;
 }
 
 int dnn_hip_session_kernel(dnn_hip_session *s, int *which) {
     if (!s || !which) return fail(DNN_HIP_EINVAL, "NULL argument");
-    *which = s->groups.empty() ? s->kernel_used : s->groups[0]->kernel_used;
+    *which = s->kernel_used;
     return DNN_HIP_OK;
 }
 
@@ -453,25 +420,19 @@ int dnn_hip_session_last_ms(dnn_hip_session *s, float *ms) {
     return DNN_HIP_OK;
 }
 
-namespace {
-
-// Validate and enqueue one launch of a session of at most MAXB rows on its
-// stream (grid capped at grid_limit when > 0); decode_finish waits for it.
-// check_only: validate the arguments, enqueue nothing.  prep: the session is
-// one group of a multi-group launch: upload its inputs, fill *prep with its
-// kernel arguments (general kernel, MAXB-row build) and launch nothing.
-int decode_launch(dnn_hip_session *s, const int *feed, int n_feed_all, const int *n_feed, int n_steps, int eos,
-                  bool want_logits, int grid_limit, bool check_only = false, DecodeArgs *prep = nullptr) {
+extern "C++" {
+int dnnhip::check_decode(dnn_hip_session *s, const int *feed, int n_feed_all, const int *n_feed, int n_steps,
+                         std::vector<int> &nf, int *nf_max) {
     dnn_hip_model *m = s->m;
     const int B = s->B;
-    std::vector<int> nf(B);
-    int nf_max = 0;
+    nf.assign(B, 0);
+    *nf_max = 0;
     for (int b = 0; b < B; b++) {
         nf[b] = n_feed ? n_feed[b] : n_feed_all;
         if (nf[b] < 1) return fail(DNN_HIP_EINVAL, "row %d: n_feed %d < 1", b, nf[b]);
-        nf_max = std::max(nf_max, nf[b]);
+        *nf_max = std::max(*nf_max, nf[b]);
     }
-    for (int t = 0; t < nf_max; t++)
+    for (int t = 0; t < *nf_max; t++)
         for (int b = 0; b < B; b++)
             if (t < nf[b] && (feed[(size_t)t * B + b] < 0 || feed[(size_t)t * B + b] >= m->V))
                 return fail(DNN_HIP_ERANGE, "token id %d at step %d row %d outside [0,%d)",
@@ -482,15 +443,29 @@ int decode_launch(dnn_hip_session *s, const int *feed, int n_feed_all, const int
         if (m->rope && s->h_pos[b] + n_steps > m->rope_rows)
             return fail(DNN_HIP_ERANGE, "row %d: position %d beyond the RoPE table (%d rows)", b, s->h_pos[b] + n_steps - 1, m->rope_rows);
     }
-    if (check_only) return DNN_HIP_OK;
+    return DNN_HIP_OK;
+}
+}  // extern "C++"
+
+namespace {
+
+// Validate and enqueue one launch of a persistent decode kernel on the
+// session's stream; decode_finish waits for it.
+int decode_launch(dnn_hip_session *s, const int *feed, int n_feed_all, const int *n_feed, int n_steps, int eos,
+                  bool want_logits) {
+    dnn_hip_model *m = s->m;
+    const int B = s->B;
+    std::vector<int> nf;
+    int nf_max = 0;
+    int rc = dnnhip::check_decode(s, feed, n_feed_all, n_feed, n_steps, nf, &nf_max);
+    if (rc) return rc;
     const int dc = m->ldD / LDALIGN;
-    const int nb = prep ? MAXB : pick_nb(B);
+    const int nb = pick_nb(B);
     HIP_TRY(hipSetDevice(m->device));
     int lds_max = 0;
     HIP_TRY(hipDeviceGetAttribute(&lds_max, hipDeviceAttributeMaxSharedMemoryPerBlock, m->device));
     int grid = s->grid_cap;
     if (s->grid_req > 0) grid = std::min(grid, s->grid_req);
-    if (grid_limit > 0) grid = std::min(grid, grid_limit);
     // decode_v3 by default; the lookahead kernel (one or two rows) on request,
     // when its schedule fits (every GEMV round in at most 3 slots of the grid's
     // non-attention workgroups) and its LDS does.
@@ -498,17 +473,14 @@ int decode_launch(dnn_hip_session *s, const int *feed, int n_feed_all, const int
     size_t shmem = 0;
     StreamArgs sa{};
     bool stream = false;
-    if (prep) {
-        kern = decode_multi_for(dc);
-        shmem = lds_bytes(nb, m->ldD, m->ldF);
-    } else if (s->kernel_pref == 5 && stream_plan(m, B, grid, lds_max, &sa) &&
+    if (s->kernel_pref == 5 && stream_plan(m, B, grid, lds_max, &sa) &&
         sa.ex.total(m->L) <= s->xa_pairs) {
         kern = decode_stream_for(nb, dc);
         shmem = (size_t)sa.lds.total;
         stream = kern != nullptr;
     }
     const int rounds = (m->D + 6) / 7 + (3 * m->D / 2 + 6) / 7 + (m->D / 2 + 6) / 7 + (m->F + 6) / 7;
-    if (!kern && !prep && nb <= 2 && s->kernel_pref == 4 && grid > B * m->H && rounds <= 3 * (grid - B * m->H) &&
+    if (!kern && nb <= 2 && s->kernel_pref == 4 && grid > B * m->H && rounds <= 3 * (grid - B * m->H) &&
         lds4_bytes(nb, m->ldD, m->ldF, m->L) <= (size_t)lds_max) {
         kern = decode_lookahead_for(nb, dc);
         shmem = lds4_bytes(nb, m->ldD, m->ldF, m->L);
@@ -518,8 +490,8 @@ int decode_launch(dnn_hip_session *s, const int *feed, int n_feed_all, const int
         shmem = lds_bytes(nb, m->ldD, m->ldF);
     }
     if (!kern) return fail(DNN_HIP_EINVAL, "d_model %d: the decode kernels cover d_model <= %d", m->D, 3 * LDALIGN);
-    s->kernel_used = stream ? 5 : (prep || kern == decode_kernel_for(nb, dc)) ? 3 : 4;
-    int rc = grow(&s->feed, &s->feed_cap, (size_t)nf_max * B);
+    s->kernel_used = stream ? 5 : kern == decode_kernel_for(nb, dc) ? 3 : 4;
+    rc = grow(&s->feed, &s->feed_cap, (size_t)nf_max * B);
     if (!rc) rc = grow(&s->ids, &s->ids_cap, (size_t)n_steps * B);
     if (!rc && want_logits) rc = grow(&s->logits, &s->logits_cap, (size_t)n_steps * B * m->V);
     if (rc) return rc;
@@ -550,18 +522,13 @@ int decode_launch(dnn_hip_session *s, const int *feed, int n_feed_all, const int
     a.layers = m->d_layers;
     a.eps_final = m->eps_final;
     a.rope = m->rope; a.rope_rows = m->rope_rows;
-    a.B = B; a.max_seq = s->max_seq;
+    a.B = B; a.max_seq = s->kv_s;
     a.kc = s->kc; a.vc = s->vc; a.xa = s->xa; a.ex = s->ex;
     a.ex.grid = s->grid_cap;
     a.pos = s->pos; a.feed = s->feed; a.n_feed = s->n_feed;
     a.ids = s->ids; a.logits = want_logits ? s->logits : nullptr;
     a.n_steps = n_steps; a.eos = eos; a.step0 = s->next_tag; a.err = s->err; a.steps_done = s->steps_done;
     s->next_tag += (unsigned)n_steps;
-    if (prep) {
-        *prep = a;
-        HIP_TRY(hipStreamSynchronize(s->stream));   // inputs in place before the shared launch
-        return DNN_HIP_OK;
-    }
     sa.a = a;
     void *kargs[] = {stream ? static_cast<void *>(&sa) : static_cast<void *>(&a)};
     HIP_TRY(hipEventRecord(s->ev0, s->stream));
@@ -592,106 +559,8 @@ int decode_finish(dnn_hip_session *s, int *ids, float *logits, int *steps_done, 
 
 int decode_finish_launch(dnn_hip_session *s, const int *feed, int n_feed_all, const int *n_feed, int n_steps, int eos,
                          int *ids, float *logits, int *steps_done) {
-    const int rc = decode_launch(s, feed, n_feed_all, n_feed, n_steps, eos, logits != nullptr, 0);
+    const int rc = decode_launch(s, feed, n_feed_all, n_feed, n_steps, eos, logits != nullptr);
     return rc ? rc : decode_finish(s, ids, logits, steps_done);
-}
-
-// A session of more than MAXB rows: its groups of at most MAXB rows decode in
-// one launch of the general kernel, the grid split evenly between them
-// (persistent launches on separate streams are not co-resident on this
-// device, so a launch per group would run them in turn); the columns of feed /
-// ids / logits are gathered and scattered per group.  With eos >= 0 a group
-// that stops early is run on (greedy, no stop) to the step where the last
-// group stopped, so every row advances the same number of steps, as in one
-// launch.
-int decode_groups(dnn_hip_session *s, const int *feed, int n_feed_all, const int *n_feed, int n_steps, int eos,
-                  int *ids, float *logits, int *steps_done) {
-    const int B = s->B, V = s->m->V, NGR = (int)s->groups.size();
-    int nf_max = 0;
-    for (int b = 0; b < B; b++) nf_max = std::max(nf_max, n_feed ? n_feed[b] : n_feed_all);
-    std::vector<std::vector<int>> gfeed(NGR), gnf(NGR), gids(NGR);
-    std::vector<std::vector<float>> glog(NGR);
-    std::vector<int> r0(NGR), done(NGR, 0), more(NGR, 0);
-    for (int gi = 0, r = 0; gi < NGR; gi++) { r0[gi] = r; r += s->groups[gi]->B; }
-    dnn_hip_session *lead = s->groups[0];
-    dnn_hip_model *m = s->m;
-    float ms = 0.f;
-    // pass 0: every group from its feed; pass 1: groups that stopped early, run on
-    for (int pass = 0; pass < 2; pass++) {
-        if (pass == 1) {
-            const int all_done = *std::max_element(done.begin(), done.end());
-            for (int gi = 0; gi < NGR; gi++) more[gi] = all_done - done[gi];
-        }
-        std::vector<int> run;
-        for (int gi = 0; gi < NGR; gi++) {
-            const int gb = s->groups[gi]->B;
-            if (pass == 0) {
-                gfeed[gi].assign((size_t)std::max(nf_max, 1) * gb, 0);
-                gnf[gi].assign(gb, 0);
-                for (int b = 0; b < gb; b++) {
-                    gnf[gi][b] = n_feed ? n_feed[r0[gi] + b] : n_feed_all;
-                    for (int t = 0; t < gnf[gi][b] && t < nf_max; t++)
-                        gfeed[gi][(size_t)t * gb + b] = feed[(size_t)t * B + r0[gi] + b];
-                }
-                run.push_back(gi);
-            } else if (more[gi] > 0) {
-                // feed each row its last id, then run greedily without a stop
-                gfeed[gi].assign(gb, 0);
-                gnf[gi].assign(gb, 1);
-                for (int b = 0; b < gb; b++) gfeed[gi][b] = ids[(size_t)(done[gi] - 1) * B + r0[gi] + b];
-                run.push_back(gi);
-            }
-        }
-        if (run.empty()) continue;
-        const int per = std::max(1, lead->grid_cap / (int)run.size());
-        // every group is validated before any input is uploaded
-        for (int gi : run) {
-            const int rc = decode_launch(s->groups[gi], gfeed[gi].data(), 0, gnf[gi].data(), pass == 0 ? n_steps : more[gi],
-                                         pass == 0 ? eos : -1, logits != nullptr, per, true);
-            if (rc) return rc;
-        }
-        MultiArgs ma{};
-        ma.n = (int)run.size();
-        ma.per = per;
-        for (int i = 0; i < ma.n; i++) {
-            const int gi = run[i];
-            const int rc = decode_launch(s->groups[gi], gfeed[gi].data(), 0, gnf[gi].data(), pass == 0 ? n_steps : more[gi],
-                                         pass == 0 ? eos : -1, logits != nullptr, per, false, &ma.a[i]);
-            if (rc) return rc;
-        }
-        const void *kern = decode_multi_for(m->ldD / LDALIGN);
-        const size_t shmem = lds_bytes(MAXB, m->ldD, m->ldF);
-        void *kargs[] = {&ma};
-        HIP_TRY(hipEventRecord(lead->ev0, lead->stream));
-        HIP_TRY(hipLaunchKernel(kern, dim3(per * ma.n), dim3(BLOCK), kargs, shmem, lead->stream));
-        HIP_TRY(hipEventRecord(lead->ev1, lead->stream));
-        HIP_TRY(hipEventSynchronize(lead->ev1));
-        float pass_ms = 0.f;
-        HIP_TRY(hipEventElapsedTime(&pass_ms, lead->ev0, lead->ev1));
-        ms += pass_ms;
-        for (int gi : run) {
-            dnn_hip_session *g = s->groups[gi];
-            const int gb = g->B, steps = pass == 0 ? n_steps : more[gi];
-            gids[gi].assign((size_t)steps * gb, 0);
-            if (logits) glog[gi].assign((size_t)steps * gb * V, 0.f);
-            int d = 0;
-            const int rc = decode_finish(g, gids[gi].data(), logits ? glog[gi].data() : nullptr, &d, false);
-            if (rc) return rc;
-            g->last_ms = pass_ms;
-            const int t0 = pass == 0 ? 0 : done[gi];
-            for (int t = 0; t < d; t++)
-                for (int b = 0; b < gb; b++) {
-                    if (ids) ids[(size_t)(t0 + t) * B + r0[gi] + b] = gids[gi][(size_t)t * gb + b];
-                    if (logits)
-                        memcpy(logits + ((size_t)(t0 + t) * B + r0[gi] + b) * V, glog[gi].data() + ((size_t)t * gb + b) * V,
-                               sizeof(float) * V);
-                }
-            if (pass == 0) done[gi] = d;
-        }
-    }
-    s->last_ms = ms;
-    if (steps_done) *steps_done = *std::max_element(done.begin(), done.end());
-    return DNN_HIP_OK;
 }
 
 }  // namespace
@@ -699,16 +568,15 @@ int decode_groups(dnn_hip_session *s, const int *feed, int n_feed_all, const int
 int dnn_hip_decode(dnn_hip_session *s, const int *feed, int n_feed_all, const int *n_feed,
                    int n_steps, int eos, int *ids, float *logits, int *steps_done) {
     if (!s || !feed) return fail(DNN_HIP_EINVAL, "NULL argument");
-    const int B = s->B;
     if (n_steps <= 0) return fail(DNN_HIP_EINVAL, "n_steps %d", n_steps);
-    if (!s->groups.empty()) {
-        if (!ids && eos >= 0) return fail(DNN_HIP_EINVAL, "a multi-group session needs ids when eos >= 0");
-        for (int b = 0; b < B; b++)
-            if ((n_feed ? n_feed[b] : n_feed_all) < 1)
-                return fail(DNN_HIP_EINVAL, "row %d: n_feed %d < 1", b, n_feed ? n_feed[b] : n_feed_all);
-        return decode_groups(s, feed, n_feed_all, n_feed, n_steps, eos, ids, logits, steps_done);
-    }
+    if (s->batched) return engine_decode(s, feed, n_feed_all, n_feed, n_steps, eos, ids, logits, steps_done);
     return decode_finish_launch(s, feed, n_feed_all, n_feed, n_steps, eos, ids, logits, steps_done);
+}
+
+int dnn_hip_prefill(dnn_hip_session *s, const float *embeds, int n_embed, const int *ids, int n_ids_max,
+                    const int *n_ids, int mode, int prefix_len, int *next_ids, float *logits) {
+    if (!s || !next_ids) return fail(DNN_HIP_EINVAL, "NULL argument");
+    return engine_prefill(s, embeds, n_embed, ids, n_ids_max, n_ids, mode, prefix_len, next_ids, logits);
 }
 
 int dnn_hip_generate(dnn_hip_model *m, const int *prompt, int P, int max_new, int eos, int *out, int *n_out) {

@@ -1,0 +1,119 @@
+// session.h -- the device model and session objects behind include/dnn_hip.h.
+// Internal: shared by the C-ABI layer (dnn_hip.cpp) and the batched engine
+// (batch_engine.cpp).
+#pragma once
+#include <hip/hip_runtime.h>
+#include <cstdint>
+#include <string>
+#include <vector>
+
+#include "../../include/dnn_hip.h"
+#include "batch.h"
+#include "decode_kernel.h"
+
+struct dnn_hip_model {
+    int V, D, L, H, dk, F, ldD, ldF;
+    int device;
+    int bf16 = 0;                    // weight matrices rounded to bf16 (W16A32)
+    char *arena = nullptr;           // fp32 weights, biases, gammas
+    uint16_t *arena16 = nullptr;     // bf16 copy of the weight matrices at the same element offsets
+    size_t arena_bytes = 0;
+    dnnhip::LayerOff *d_layers = nullptr;    // [L] float offsets of each block's tensors
+    std::vector<dnnhip::LayerOff> h_layers;
+    float eps_final = 1e-5f;
+    std::vector<float> eps;          // 2L+1
+    float *rope = nullptr;           // [2][rope_rows][dk/2]: cos, then sin
+    int rope_rows = 0;
+    // byte offsets of every device tensor inside the arena, for the uploads
+    struct Off { size_t embed, lm_bias, g_final; std::vector<size_t> l; } off;
+};
+
+// Buffers of the batched engine (one per session that uses it).
+struct BatchEngine {
+    int mcap = 0;                    // rows the activation buffers hold
+    float *X = nullptr, *X1 = nullptr, *ATT = nullptr, *Q = nullptr, *ACT = nullptr;
+    uint2 *part = nullptr;           // split-K partials of the decode GEMMs
+    size_t part_pairs = 0;
+    uint2 *apart = nullptr;          // split attention partials
+    size_t apart_pairs = 0;
+    uint2 *amax = nullptr;           // lm_head argmax partials
+    size_t amax_pairs = 0;
+    unsigned *cnt = nullptr;         // last-arriver counters: [0, CNT_ATT) GEMM tiles, then attention, then head
+    dnnhip::StepState *st = nullptr;
+    int *row_ident = nullptr;        // [64] 0..63
+    int *row_done = nullptr;         // [64]
+    int *steps_done = nullptr;
+    // prefill inputs
+    int *pre_i = nullptr;            // row_b, row_p, pid [mcap] each, then row0, n_new, p0, arow [64], tiles
+    size_t pre_cap = 0;
+    int *next_ids = nullptr;         // [64]
+    float *pre_logits = nullptr;     // [64][V]
+    // the captured decode step
+    hipGraphExec_t gexec = nullptr;
+    const void *gkey[4] = {nullptr, nullptr, nullptr, nullptr};
+    int geos = -2;
+};
+
+struct dnn_hip_session {
+    dnn_hip_model *m;
+    int B, max_seq;
+    int kv_s = 0;                             // KV row stride in positions (max_seq rounded up to 64)
+    int batched = 0;                          // decode runs on the batched engine
+    hipStream_t stream = nullptr;
+    hipEvent_t ev0 = nullptr, ev1 = nullptr;
+    float *kc = nullptr, *vc = nullptr;       // K^T [L][B][H][DK][kv_s], V [L][B][H][kv_s][DK]
+    uint2 *xa = nullptr;                      // exchange arena (tagged pairs)
+    dnnhip::Exch ex{};
+    int *pos = nullptr, *steps_done = nullptr, *err = nullptr;
+    int *feed = nullptr, *n_feed = nullptr, *ids = nullptr;
+    size_t feed_cap = 0, ids_cap = 0;
+    float *logits = nullptr;
+    size_t logits_cap = 0;
+    int grid_req = 0, grid = 0, grid_cap = 0;
+    unsigned next_tag = 1;                    // tags only grow: stale values never match
+    int kernel_pref = 0;                      // env DNN_HIP_DECODE_KERNEL: 4 / 5 / 6: lookahead / streaming / batched engine
+    int kernel_used = 0;                      // 3, 4, 5 or 6: the kernel of the last launch
+    size_t xa_pairs = 0;
+    float last_ms = 0.f;
+    std::vector<int> h_pos;
+    BatchEngine *eng = nullptr;
+};
+
+namespace dnnhip {
+
+// error helpers shared by the C-ABI translation units
+int set_error(int code, const char *fmt, ...);
+
+template <class T>
+int dalloc(T **p, size_t count) {
+    hipError_t e = hipMalloc(reinterpret_cast<void **>(p), (count ? count : 1) * sizeof(T));
+    if (e != hipSuccess) {
+        *p = nullptr;
+        return set_error(DNN_HIP_ENOMEM, "hipMalloc(%zu bytes): %s", count * sizeof(T), hipGetErrorString(e));
+    }
+    return DNN_HIP_OK;
+}
+
+template <class T>
+int grow(T **p, size_t *cap, size_t count) {
+    if (count <= *cap) return DNN_HIP_OK;
+    if (*p) (void)hipFree(*p);
+    *p = nullptr;
+    *cap = 0;
+    int rc = dalloc(p, count);
+    if (rc == DNN_HIP_OK) *cap = count;
+    return rc;
+}
+
+// argument checks of dnn_hip_decode: nf[b] = feed rows of row b
+int check_decode(dnn_hip_session *s, const int *feed, int n_feed_all, const int *n_feed, int n_steps,
+                 std::vector<int> &nf, int *nf_max);
+
+// batched engine (batch_engine.cpp)
+int engine_decode(dnn_hip_session *s, const int *feed, int n_feed_all, const int *n_feed, int n_steps, int eos,
+                  int *ids, float *logits, int *steps_done);
+int engine_prefill(dnn_hip_session *s, const float *embeds, int n_embed, const int *ids, int n_ids_max,
+                   const int *n_ids, int mode, int prefix_len, int *next_ids, float *logits);
+void engine_destroy(BatchEngine *e);
+
+}  // namespace dnnhip

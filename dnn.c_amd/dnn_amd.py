@@ -23,8 +23,11 @@ HIP_SYMBOLS = [
     "dnn_hip_model_rope", "dnn_hip_model_destroy", "dnn_hip_session_create",
     "dnn_hip_session_reset", "dnn_hip_session_lengths", "dnn_hip_session_destroy",
     "dnn_hip_decode", "dnn_hip_generate", "dnn_hip_session_last_ms", "dnn_hip_session_set_grid",
-    "dnn_hip_session_grid", "dnn_hip_session_kernel",
+    "dnn_hip_session_grid", "dnn_hip_session_kernel", "dnn_hip_model_create_ex", "dnn_hip_prefill",
 ]
+
+WEIGHTS_F32 = 0
+WEIGHTS_BF16 = 1
 
 
 class HipError(RuntimeError):
@@ -57,6 +60,9 @@ def hip():
         L.dnn_hip_session_set_grid.argtypes = [C.c_void_p, C.c_int]
         L.dnn_hip_session_grid.argtypes = [C.c_void_p, i32p]
         L.dnn_hip_session_kernel.argtypes = [C.c_void_p, i32p]
+        L.dnn_hip_model_create_ex.argtypes = [C.c_int] * 6 + [C.POINTER(f32p), C.c_int, f32p, C.c_int,
+                                                              C.POINTER(C.c_void_p)]
+        L.dnn_hip_prefill.argtypes = [C.c_void_p, f32p, C.c_int, i32p, C.c_int, i32p, C.c_int, C.c_int, i32p, f32p]
         _hip = L
     return _hip
 
@@ -77,13 +83,13 @@ def _ip(a):
 class HipModel:
     """HBM mirror of a decoder LM given its parameters in module order."""
 
-    def __init__(self, V, D, L, H, F, params, rope=None, dk=64):
+    def __init__(self, V, D, L, H, F, params, rope=None, dk=64, weights=WEIGHTS_F32):
         params = [np.ascontiguousarray(p, dtype=np.float32) for p in params]
         self._keep = params
         arr = (f32p * len(params))(*[_fp(p) for p in params])
         h = C.c_void_p()
         check(hip().dnn_hip_init(0))
-        check(hip().dnn_hip_model_create(V, D, L, H, dk, F, arr, len(params), None, C.byref(h)))
+        check(hip().dnn_hip_model_create_ex(V, D, L, H, dk, F, arr, len(params), None, weights, C.byref(h)))
         self.ptr = h
         self.V, self.D, self.L, self.H, self.F = V, D, L, H, F
         if rope is not None:
@@ -123,7 +129,7 @@ class HipSession:
         return g.value
 
     def kernel(self):
-        """3 or 4: the decode kernel of the last decode() call."""
+        """3..6: the decode kernel of the last decode() call (6: the batched engine)."""
         k = C.c_int()
         check(hip().dnn_hip_session_kernel(self.ptr, C.byref(k)))
         return k.value
@@ -142,6 +148,29 @@ class HipSession:
                                    n_steps, eos, _ip(ids), _fp(lg) if want_logits else None, C.byref(done)))
         d = done.value
         return ids[:d], (lg[:d] if want_logits else None)
+
+    def prefill(self, ids=None, n_ids=None, embeds=None, mode=0, prefix_len=0, want_logits=False):
+        """Multi-token prefill.  ids: [B][n_max] ints (or None), n_ids: [B] or None,
+        embeds: [B][n_embed][D] floats or None.  Returns (next_ids [B], logits [B][V] or None)."""
+        B = self.B
+        if ids is None:
+            ids_a, n_max = None, 0
+        else:
+            ids_a = np.ascontiguousarray(ids, dtype=np.int32).reshape(B, -1)
+            n_max = ids_a.shape[1]
+        nid = None if n_ids is None else np.ascontiguousarray(n_ids, dtype=np.int32)
+        if embeds is None:
+            emb, n_emb = None, 0
+        else:
+            emb = np.ascontiguousarray(embeds, dtype=np.float32).reshape(B, -1, self.m.D)
+            n_emb = emb.shape[1]
+        nxt = np.zeros(B, dtype=np.int32)
+        lg = np.zeros((B, self.m.V), dtype=np.float32) if want_logits else None
+        check(hip().dnn_hip_prefill(self.ptr, _fp(emb) if emb is not None else None, n_emb,
+                                    _ip(ids_a) if ids_a is not None else None, n_max,
+                                    _ip(nid) if nid is not None else None, mode, prefix_len, _ip(nxt),
+                                    _fp(lg) if want_logits else None))
+        return nxt, lg
 
     def last_ms(self):
         ms = C.c_float()

@@ -71,6 +71,21 @@ int dnn_hip_model_create(int vocab_size, int d_model, int n_layers, int n_heads,
                          const float *const *params, int n_params,
                          const float *eps, dnn_hip_model **out);
 
+/* Weight storage of a device model. */
+#define DNN_HIP_WEIGHTS_F32   0
+/* Every weight matrix (embedding / tied lm_head, qkv, out, gate, up, down)
+ * rounded to bf16 (round to nearest even) and streamed as bf16; biases, RMSNorm
+ * gammas and all arithmetic stay fp32 (W16A32).  The reference is fp32-only:
+ * this is the fp32 model on bf16-rounded weights.  Decode of such a model runs
+ * on the batched engine. */
+#define DNN_HIP_WEIGHTS_BF16  1
+
+/* dnn_hip_model_create with a choice of weight storage (DNN_HIP_WEIGHTS_*). */
+int dnn_hip_model_create_ex(int vocab_size, int d_model, int n_layers, int n_heads,
+                            int d_k, int intermediate_size,
+                            const float *const *params, int n_params,
+                            const float *eps, int weights, dnn_hip_model **out);
+
 /* Re-uploads the parameters of an existing model (same shapes). */
 int dnn_hip_model_update(dnn_hip_model *m, const float *const *params, int n_params);
 
@@ -83,9 +98,10 @@ int dnn_hip_model_destroy(dnn_hip_model *m);
 /* A decode session: the per-layer KV caches of `batch` rows in HBM (K stored
  * transposed, [L][B][H][d_k][max_seq]; V as [L][B][H][max_seq][d_k]) plus the
  * exchange arena of the decode kernel.  Every row starts empty.
- * 1 <= batch <= 64.  A session of more than 8 rows holds groups of at most
- * 8 rows; dnn_hip_decode runs them in one launch, the grid split between
- * them. */
+ * 1 <= batch <= 64.  Sessions of at most 8 rows decode with one persistent
+ * kernel launch per call; sessions of more rows (and every session of a bf16
+ * model) decode on the batched engine, one replay of a captured HIP graph per
+ * step, every weight read once per step for all rows. */
 int dnn_hip_session_create(dnn_hip_model *m, int batch, int max_seq,
                            dnn_hip_session **out);
 /* Empties every row (lengths back to 0). */
@@ -107,6 +123,24 @@ int dnn_hip_decode(dnn_hip_session *s, const int *feed, int n_feed_all,
                    const int *n_feed, int n_steps, int eos, int *ids,
                    float *logits, int *steps_done);
 
+/* Multi-token cached prefill of every row: transformer_block_forward_cached_ex
+ * over all layers for N new rows per sequence (transformer.c:211-416, the
+ * multi-token form of the prompt loop gpt.c:306-344, and the prefix prefill of
+ * vision_lm_generate vlm.c:497-517), then the final rms_norm, tied lm_head and
+ * argmax of each row's last new position.
+ *   row b's new rows: n_embed input rows embeds[b][0..n_embed)[d_model] (e.g.
+ *   image patch embeddings; NULL when n_embed = 0), then n_ids[b] tokens
+ *   ids[b * n_ids_max + t] (n_ids NULL: n_ids_max each), embedded by the model.
+ *   mode 0: causal (row at position p sees keys <= p); mode 1: prefix-LM
+ *   (ATTENTION_PREFIX_LM, transformer.c:313-323: a row at p < prefix_len sees
+ *   keys < prefix_len, later rows keys <= p), which needs empty rows.
+ * next_ids[b] gets the argmax of row b's last new position, logits (nullable)
+ * [batch][V] its logits.  Each row's length grows by its new rows; a following
+ * dnn_hip_decode(s, next_ids, 1, ...) continues greedily. */
+int dnn_hip_prefill(dnn_hip_session *s, const float *embeds, int n_embed,
+                    const int *ids, int n_ids_max, const int *n_ids,
+                    int mode, int prefix_len, int *next_ids, float *logits);
+
 /* decoder_lm_generate(use_cache=1, temperature=0) for one sequence: out gets
  * prompt + generated ids (P + max_new ints), *n_out its length (stops after eos
  * when eos >= 0).  Uses a fresh session of max_seq = P + max_new. */
@@ -124,10 +158,11 @@ int dnn_hip_session_set_grid(dnn_hip_session *s, int n_workgroups);
 /* Workgroups the last dnn_hip_decode launch on this session used. */
 int dnn_hip_session_grid(dnn_hip_session *s, int *n_workgroups);
 /* Which decode kernel the last dnn_hip_decode launch used: 3 = the general
- * one (up to 8 rows, the default), 4 = the layer-lookahead kernel, 5 = the
- * streaming kernel (both 1-2 rows), chosen when the environment variable
+ * persistent one (up to 8 rows, the default), 4 = the layer-lookahead kernel,
+ * 5 = the streaming kernel (both 1-2 rows), chosen when the environment variable
  * DNN_HIP_DECODE_KERNEL is 4 or 5 at session creation and the kernel's
- * schedule fits the model and grid. */
+ * schedule fits the model and grid; 6 = the batched engine (more than 8 rows,
+ * bf16 weights, or DNN_HIP_DECODE_KERNEL=6). */
 int dnn_hip_session_kernel(dnn_hip_session *s, int *which);
 
 #ifdef __cplusplus

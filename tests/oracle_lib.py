@@ -108,6 +108,19 @@ class Model:
             out.append(np.ctypeslib.as_array(p, shape=(n.value,)).copy())
         return out
 
+    def round_weights_bf16(self):
+        """Rounds every weight matrix (embedding, qkv, out, gate, up, down) to
+        bf16 in place (round to nearest even, stored back as fp32): the W16A32
+        model a bf16-weight device model computes.  Biases and gammas stay."""
+        mats = [0] + [1 + 12 * l + k for l in range(self.L) for k in (0, 2, 6, 8, 10)]
+        for i in mats:
+            n = C.c_longlong()
+            p = lib().orc_model_param(self.ptr, i, C.byref(n))
+            a = np.ctypeslib.as_array(p, shape=(n.value,))
+            u = a.view(np.uint32)
+            r = ((u.astype(np.uint64) + 0x7FFF + ((u >> 16) & 1)) >> 16).astype(np.uint32) << 16
+            u[:] = r
+
     def rope_tables(self):
         rows = lib().orc_model_rope_rows(self.ptr)
         if rows == 0:

@@ -1,0 +1,177 @@
+"""GPU parity of the batched engine (more than 8 rows, bf16 weights, multi-token
+prefill) against the oracle and the reference's fixtures.
+
+Bars: greedy tokens identical; logits within
+max-abs 1e-3 and relative 1e-4 (max |dlogit| / max |logit| per row).  The bf16
+variant is checked against the oracle run on the same bf16-rounded weights
+(W16A32), to the same bar: only the summation order differs.
+"""
+import numpy as np
+import pytest
+
+import dnn_amd as A
+import oracle_lib as O
+from golden_util import binf
+from test_parity_gpu import assert_logits_close, hip_model
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.fixture(scope="module")
+def c1g():
+    return O.Model(128, 256, 4, 4, 683, 256, seed=11, init="gpt2")
+
+
+@pytest.mark.parametrize("B", [16, 33, 64])
+def test_engine_rows_match_independent_runs(c1g, B):
+    """Every row of a batched decode (the engine: more than 8 rows) equals its
+    own B=1 oracle run; rows switch from prompt to greedy at different steps."""
+    hm = hip_model(c1g)
+    rng = np.random.default_rng(100 + B)
+    lens = rng.integers(1, 9, size=B).astype(np.int32)
+    feed = rng.integers(0, 128, size=(8, B)).astype(np.int32)
+    steps = 40
+    print("engine rows B=%d" % B, flush=True)
+    s = A.HipSession(hm, B, 72)
+    ids, lg = s.decode(feed, steps, n_feed=lens, want_logits=True)
+    assert s.kernel() == 6
+    for b in range(B):
+        want, wlg = c1g.generate(feed[: lens[b], b], steps - lens[b] + 1, eos=-1, want_logits=True)
+        got = list(feed[: lens[b], b]) + list(ids[lens[b] - 1:, b])
+        assert got == list(want), "row %d" % b
+        assert_logits_close(lg[lens[b] - 1:, b], wlg, "row %d" % b)
+    assert list(s.lengths()) == [steps] * B
+    # a second call continues every row from its cached length
+    ids2, _ = s.decode(ids[-1:], 8)
+    for b in range(B):
+        want = c1g.generate(feed[: lens[b], b], steps - lens[b] + 9, eos=-1)
+        assert list(ids2[:, b]) == list(want[steps + 1:steps + 9]), "row %d, second call" % b
+
+
+def test_engine_c2_tokens_and_logits_match_reference(golden, monkeypatch):
+    """The C2 model on the engine (one row, forced): the reference's own greedy
+    tokens and its logits of the first four generated steps."""
+    m = O.Model(8192, 768, 12, 12, 2048, 1088, seed=2)
+    hm = hip_model(m)
+    monkeypatch.setenv("DNN_HIP_DECODE_KERNEL", "6")
+    toks = golden["c2_tokens"]
+    s = A.HipSession(hm, 1, 200)
+    ids, _ = s.decode(np.array(toks[:32], dtype=np.int32), 160, n_feed=np.array([32], np.int32))
+    assert s.kernel() == 6
+    assert list(ids[31:, 0]) == toks[32:161]
+    s2 = A.HipSession(hm, 1, 64)
+    _, lg = s2.decode(np.array(toks[:35], dtype=np.int32), 35, want_logits=True)
+    assert_logits_close(lg[31:, 0], binf("c2_logits4.f32", 8192), "c2 first 4 steps (engine)")
+
+
+def test_engine_equals_persistent_kernel_c2_b8(golden, monkeypatch):
+    """Eight C2 rows: the engine's tokens equal the persistent kernel's and its
+    logits agree within the bar (different summation order)."""
+    m = O.Model(8192, 768, 12, 12, 2048, 1088, seed=2)
+    hm = hip_model(m)
+    rng = np.random.default_rng(8)
+    feed = rng.integers(0, 8192, size=(6, 8)).astype(np.int32)
+    monkeypatch.setenv("DNN_HIP_DECODE_KERNEL", "3")
+    s3 = A.HipSession(hm, 8, 64)
+    ids3, lg3 = s3.decode(feed, 40, want_logits=True)
+    monkeypatch.setenv("DNN_HIP_DECODE_KERNEL", "6")
+    s6 = A.HipSession(hm, 8, 64)
+    ids6, lg6 = s6.decode(feed, 40, want_logits=True)
+    assert s3.kernel() == 3 and s6.kernel() == 6
+    assert np.array_equal(ids3, ids6)
+    for b in range(8):
+        assert_logits_close(lg6[:, b], lg3[:, b], "row %d" % b)
+
+
+@pytest.mark.parametrize("B", [1, 5, 12])
+def test_prefill_causal_matches_cached_forward(c1g, B):
+    """dnn_hip_prefill over ragged prompts (some longer than one 64-row tile)
+    equals the oracle's multi-token cached forward (transformer.c:211-416) at
+    each row's last position; decoding on from there equals the oracle's
+    generation from the same prompt."""
+    hm = hip_model(c1g)
+    rng = np.random.default_rng(200 + B)
+    n = rng.integers(1, 150, size=B).astype(np.int32)
+    ids = rng.integers(0, 128, size=(B, int(n.max()))).astype(np.int32)
+    print("prefill causal B=%d n=%s" % (B, list(n)), flush=True)
+    s = A.HipSession(hm, B, 200)
+    nxt, lg = s.prefill(ids=ids, n_ids=n, want_logits=True)
+    assert list(s.lengths()) == list(n)
+    for b in range(B):
+        st = O.State(c1g, 200)
+        h = st.forward(O.embed(c1g, ids[b, : n[b]]))
+        want = O.head(c1g, h[-1:])
+        assert_logits_close(lg[b:b + 1], want, "row %d prefill" % b)
+        assert nxt[b] == int(np.argmax(want[0]))
+    out, _ = s.decode(nxt, 20)
+    for b in range(B):
+        want = c1g.generate(ids[b, : n[b]], 21, eos=-1)
+        assert [int(nxt[b])] + list(out[:, b]) == list(want[n[b]:]), "row %d decode after prefill" % b
+
+
+def test_prefill_c2_long_prompt(golden):
+    """C2: a 288-token prompt prefilled at once (five 64-row tiles, 288-key
+    causal attention) against the oracle's cached forward."""
+    m = O.Model(8192, 768, 12, 12, 2048, 1088, seed=2)
+    hm = hip_model(m)
+    toks = np.array(golden["c2_tokens"][:288], dtype=np.int32)
+    s = A.HipSession(hm, 1, 320)
+    nxt, lg = s.prefill(ids=toks[None, :], want_logits=True)
+    st = O.State(m, 288)
+    h = st.forward(O.embed(m, toks))
+    want = O.head(m, h[-1:])
+    assert_logits_close(lg, want, "c2 prefill 288")
+    assert nxt[0] == golden["c2_tokens"][288]
+
+
+@pytest.mark.parametrize("B", [3, 16])
+def test_prefill_prefix_lm(B):
+    """Prefix-LM prefill (the VLM shape, vlm.c:497-517): embedding rows as a
+    bidirectional prefix, then causal text tokens, ragged per row; against the
+    oracle's prefix-LM cached forward (transformer.c:313-323), then greedy
+    decode on from the prefill against the oracle continuing the same state."""
+    V, D, L, H, F = 256, 128, 2, 2, 256
+    m = O.Model(V, D, L, H, F, 128, seed=5, init="gpt2")
+    hm = hip_model(m)
+    rng = np.random.default_rng(300 + B)
+    I = 70
+    emb = rng.standard_normal((B, I, D)).astype(np.float32)
+    n = rng.integers(1, 5, size=B).astype(np.int32)
+    ids = rng.integers(0, V, size=(B, 4)).astype(np.int32)
+    s = A.HipSession(hm, B, 128)
+    nxt, lg = s.prefill(ids=ids, n_ids=n, embeds=emb, mode=1, prefix_len=I, want_logits=True)
+    assert list(s.lengths()) == list(I + n)
+    out, olg = s.decode(nxt, 6, want_logits=True)
+    for b in range(B):
+        st = O.State(m, 128)
+        x = np.concatenate([emb[b], O.embed(m, ids[b, : n[b]])])
+        h = st.forward(x, mode=1, prefix_len=I)
+        want = O.head(m, h[-1:])
+        assert_logits_close(lg[b:b + 1], want, "row %d prefix prefill" % b)
+        tok = int(np.argmax(want[0]))
+        assert nxt[b] == tok
+        for t in range(6):
+            h = st.forward(O.embed(m, np.array([tok], np.int32)))
+            w = O.head(m, h)
+            assert_logits_close(olg[t, b:b + 1], w, "row %d decode step %d" % (b, t))
+            tok = int(np.argmax(w[0]))
+            assert out[t, b] == tok, "row %d step %d" % (b, t)
+
+
+@pytest.mark.parametrize("B", [1, 20])
+def test_bf16_weights_match_rounded_oracle(B):
+    """bf16 weight storage (W16A32, no reference counterpart): tokens and
+    logits equal the oracle's fp32 arithmetic on the same bf16-rounded weights,
+    to the same bar."""
+    m = O.Model(128, 256, 4, 4, 683, 128, seed=11, init="gpt2")
+    m.round_weights_bf16()
+    hm = A.HipModel(m.V, m.D, m.L, m.H, m.F, m.params(), rope=m.rope_tables(), weights=A.WEIGHTS_BF16)
+    rng = np.random.default_rng(400 + B)
+    feed = rng.integers(0, 128, size=(6, B)).astype(np.int32)
+    s = A.HipSession(hm, B, 64)
+    ids, lg = s.decode(feed, 30, want_logits=True)
+    assert s.kernel() == 6
+    for b in range(B):
+        want, wlg = m.generate(feed[:, b], 25, eos=-1, want_logits=True)
+        assert list(ids[5:, b]) == list(want[6:]), "row %d" % b
+        assert_logits_close(lg[5:, b], wlg, "row %d" % b)

@@ -213,11 +213,11 @@ def test_large_batch_is_refused(c1g):
 
 
 def test_multi_group_eos_keeps_rows_in_step(c1g):
-    """More than 8 rows run as groups of 8.  With an EOS stop, a group that
-    finishes before the others is run on greedily, so every row advances the
-    same number of steps and each row's ids equal its own independent run.
-    Rows 8..11 (the second group) share one prompt and rows 0..7 another; the
-    EOS id is one the second prompt emits early and the first never does."""
+    """More than 8 rows (the batched engine) with an EOS stop: rows that emit
+    EOS early are run on greedily while others have not, so every row advances
+    the same number of steps and each row's ids equal its own independent run.
+    Rows 8..11 share one prompt and rows 0..7 another; the EOS id is one the
+    second prompt emits early and the first never does."""
     hm = hip_model(c1g)
     B, steps = 12, 40
     rng = np.random.default_rng(7)
