@@ -27,6 +27,7 @@ constexpr int BK_MAXM = 64;        // rows of the decode GEMM shape (all rows in
 constexpr int BK_PBM = 128;        // prefill GEMM tile rows
 constexpr int BK_PBN = 128;        // prefill GEMM tile columns
 constexpr int BK_SEQ_ALIGN = 64;   // KV cache row stride is a multiple of this many positions
+constexpr int BK_MAXD = 768;       // d_model the engine covers
 
 enum BatchEpi { EPI_QKV = 0, EPI_RES = 1, EPI_SWIGLU = 2, EPI_HEAD = 3 };
 
@@ -51,6 +52,7 @@ struct GemmArgs {
     size_t w_bytes;             // bytes from W to the end of its arena (loads past it read 0)
     int ldw, N, K;
     int ks;                     // workgroups per column tile (split K), >= 1
+    int mt_max;                 // decode shape: at most this many 16-row tiles per workgroup (0: all rows)
     const float *bias, *bias2;  // [N] (gate/up: bias = gate biases [N/2], bias2 = up biases)
     const float *gamma;         // rms_norm gamma [K] or null
     float eps;
@@ -68,13 +70,14 @@ struct GemmArgs {
     const float *rope;          // [2][rope_rows][DK/2] or null
     int rope_rows;
     // split-K partials and last-arriver counters
-    uint2 *part;                // [ks][M][N] tagged pairs
+    uint2 *part;                // [ks][M][N] tagged pairs, then [column tiles][ks][M] row sums of squares
     unsigned *cnt;              // per column tile
     StepState *st;
     int kslot;                  // distinct per launch of a step: tags are tag * 128 + kslot
     // HEAD
-    uint2 *amax;                // [M][n tiles] (value bits, index | tag << 16)
-    unsigned *head_cnt;         // one counter
+    uint2 *amax;                // [M][column tiles] (value bits, index) per lm_head tile
+    unsigned *head_cnt;         // last-arriver counter of head_finish_kernel
+    int amax_tiles;             // column tiles of the lm_head GEMM (partials per row)
     float *logits;              // [steps][M][V] or null
     int *ids;                   // [steps][M]
     const int *feed, *n_feed;   // [*][M], [M]
@@ -132,7 +135,10 @@ struct EmbedArgs {
 // host-side launchers (batch_kernels.hip); all enqueue on `stream` and return
 // a hipError_t.  bf16: W holds bf16 weights.
 hipError_t launch_gemm(int epi, bool norm, bool bf16, bool prefill, const GemmArgs &g, hipStream_t stream);
+hipError_t launch_head_finish(const GemmArgs &g, hipStream_t stream);
 hipError_t launch_attn(const AttnArgs &a, hipStream_t stream);
+// k-steps per wavefront the decode GEMM is built for
+constexpr int GEMM_KPW[] = {12, 8, 6, 4, 3, 2};
 hipError_t launch_prefill_attn(const PrefillAttnArgs &a, hipStream_t stream);
 hipError_t launch_embed(const EmbedArgs &a, hipStream_t stream);
 int gemm_tile_rows(bool prefill, int M);

@@ -37,20 +37,38 @@ constexpr int CNT_TOTAL = CNT_GEMM + CNT_ATT + 1;
 
 inline int round_up(int v, int a) { return (v + a - 1) / a * a; }
 
-// workgroups per column tile of a decode GEMM: every wavefront's k-steps a
-// multiple of 4 (the kernel's unroll), at least 256 workgroups where possible
-int pick_ks(int ntiles, int K) {
-    const int nks = K / 16;
-    int best = 1;
-    for (int ks = 1; ks <= 8; ks++) {
-        if (nks % (16 * ks)) continue;
+// Split of a decode GEMM: k-steps per wavefront (kpw, one of GEMM_KPW) and
+// workgroups per column tile (ks), K/16 = 4 * ks * kpw.  A wavefront holds all
+// of its A and W loads in registers at once, which bounds kpw by the row tiles
+// per workgroup (mt_max, 0 = all); a GEMM without rms_norm is split further
+// until it has 64 workgroups (the split's partials and last-arriver cost more
+// than the extra parallelism gains below that).
+int pick_ks(int ntiles, int K, int M, bool norm, int mt_max = 0) {
+    const int nks = K / 16, tiles_m = (M + 15) / 16;
+    const int mt = mt_max > 0 && tiles_m > mt_max ? mt_max : tiles_m;
+    const int row_groups = (tiles_m + mt - 1) / mt;
+    static const int lim_norm[4] = {19, 14, 11, 9}, lim_plain[4] = {28, 19, 14, 11};
+    const int lim = (norm ? lim_norm : lim_plain)[mt - 1];
+    int best = 0;
+    for (int kpw : GEMM_KPW) {
+        if (kpw > lim || nks % (4 * kpw)) continue;
+        const int ks = nks / (4 * kpw);
+        if (ks > 8) break;
         best = ks;
-        if (ntiles * ks >= 256) break;
+        if (norm || ntiles * ks * row_groups >= 64) break;
     }
     return best;
 }
 
-int attn_splits(int M, int H) { return std::max(1, std::min(8, 768 / (M * H))); }
+// workgroups per (row, head) of the decode attention: one where the rows and
+// heads alone fill the chip
+int attn_splits(int M, int H) { return M * H >= 256 ? 1 : std::min(8, (256 + M * H - 1) / (M * H)); }
+
+// Split-K partial pairs a decode GEMM of these dimensions needs.
+size_t part_pairs_for(int N, int K, int M, bool norm, int mt_max = 0) {
+    const int ntn = (N + 15) / 16, ks = pick_ks(ntn, K, M, norm, mt_max);
+    return ks > 1 ? (size_t)ks * M * N + (size_t)ntn * ks * M : 0;
+}
 
 void free_acts(BatchEngine *e) {
     float *bufs[] = {e->X, e->X1, e->ATT, e->Q, e->ACT};
@@ -76,8 +94,13 @@ int engine_get(dnn_hip_session *s, int rows) {
     if (!e) {
         e = s->eng = new BatchEngine();
         const int ntn_head = (m->V + 15) / 16;
-        const int ks_max = 8;
-        e->part_pairs = (size_t)ks_max * MAX_ROWS * m->D;
+        e->part_pairs = 1;
+        for (int rows = 16; rows <= MAX_ROWS; rows += 16) {
+            const size_t need[5] = {part_pairs_for(3 * m->D, m->ldD, rows, true), part_pairs_for(m->D, m->ldD, rows, false, 1),
+                                    part_pairs_for(2 * m->F, m->ldD, rows, true), part_pairs_for(m->D, m->ldF, rows, false),
+                                    part_pairs_for(m->V, m->ldD, rows, true)};
+            for (size_t n : need) e->part_pairs = std::max(e->part_pairs, n);
+        }
         e->apart_pairs = (size_t)MAX_ROWS * m->H * 8 * (BK_DK + 2);
         e->amax_pairs = (size_t)MAX_ROWS * ntn_head;
         int rc = 0;
@@ -174,6 +197,8 @@ int enqueue_layer(dnn_hip_session *s, int l, const PrefillPlan *pp) {
 
     GemmArgs g = gemm_base(s, W, lo.wqkv, ldD, 3 * D, ldD);
     g.A = e->X; g.lda = ldD; g.M = M;
+    g.ks = pre ? 1 : pick_ks((3 * D + 15) / 16, ldD, M, true);
+    g.part = e->part; g.cnt = e->cnt;
     g.bias = W.f(lo.bqkv);
     g.gamma = W.f(lo.g_attn); g.eps = lo.eps_attn; g.dnorm = D;
     g.q = e->Q; g.kc = s->kc; g.vc = s->vc;
@@ -204,7 +229,8 @@ int enqueue_layer(dnn_hip_session *s, int l, const PrefillPlan *pp) {
     g.A = e->ATT; g.lda = ldD; g.M = M;
     g.bias = W.f(lo.bo);
     g.out = e->X1; g.ldo = ldD; g.res = e->X; g.ldr = ldD;
-    g.ks = pre ? 1 : pick_ks((D + 15) / 16, ldD);
+    g.mt_max = 1;          // out_proj: one 16-row tile per workgroup (more, lighter workgroups)
+    g.ks = pre ? 1 : pick_ks((D + 15) / 16, ldD, M, false, g.mt_max);
     g.part = e->part; g.cnt = e->cnt; g.kslot = 5 * l + 2;
     HIP_TRY(launch_gemm(EPI_RES, false, bf, pre, g, s->stream));
 
@@ -213,6 +239,8 @@ int enqueue_layer(dnn_hip_session *s, int l, const PrefillPlan *pp) {
     g.bias = W.f(lo.bg); g.bias2 = W.f(lo.bu);
     g.gamma = W.f(lo.g_ffn); g.eps = lo.eps_ffn; g.dnorm = D;
     g.out = e->ACT; g.ldo = ldF;
+    g.ks = pre ? 1 : pick_ks((2 * m->F + 15) / 16, ldD, M, true);
+    g.part = e->part; g.cnt = e->cnt;
     g.kslot = 5 * l + 3;
     HIP_TRY(launch_gemm(EPI_SWIGLU, true, bf, pre, g, s->stream));
 
@@ -220,7 +248,7 @@ int enqueue_layer(dnn_hip_session *s, int l, const PrefillPlan *pp) {
     g.A = e->ACT; g.lda = ldF; g.M = M;
     g.bias = W.f(lo.bd);
     g.out = e->X; g.ldo = ldD; g.res = e->X1; g.ldr = ldD;
-    g.ks = pre ? 1 : pick_ks((D + 15) / 16, ldF);
+    g.ks = pre ? 1 : pick_ks((D + 15) / 16, ldF, M, false);
     g.part = e->part; g.cnt = e->cnt; g.kslot = 5 * l + 4;
     HIP_TRY(launch_gemm(EPI_RES, false, bf, pre, g, s->stream));
     return DNN_HIP_OK;
@@ -245,7 +273,11 @@ int enqueue_head(dnn_hip_session *s, const PrefillPlan *pp, float *logits, int *
     g.steps_done = e->steps_done; g.eos = eos; g.row_done = e->row_done;
     g.prefill = pp != nullptr;
     g.kslot = 5 * m->L;
+    g.ks = pick_ks((m->V + 15) / 16, m->ldD, s->B, true);
+    g.amax_tiles = (m->V + 15) / 16;
+    g.part = e->part; g.cnt = e->cnt;
     HIP_TRY(launch_gemm(EPI_HEAD, true, m->bf16 != 0, false, g, s->stream));
+    HIP_TRY(launch_head_finish(g, s->stream));
     return DNN_HIP_OK;
 }
 

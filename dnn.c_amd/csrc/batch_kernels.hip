@@ -43,6 +43,7 @@ namespace dnnhip {
 namespace {
 
 constexpr int NTHR = 256;
+constexpr int ATHR = 256;                              // decode attention: four wavefronts
 
 __device__ __forceinline__ f4 mfma4(float a, float b, f4 c) {
     return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
@@ -106,24 +107,35 @@ __device__ __forceinline__ bool step_done(const StepState *st) {
 
 // ---------------------------------------------------------------------------
 // GEMM.  MT x NT 16x16 tiles per wavefront, WM x WN wavefronts over the block
-// tile, KW wavefronts splitting K; MT*NT... WM*WN*KW == 4.
-template <int MT, int NT, int WM, int WN, int KW, bool BF, int EPI, bool NORM>
+// tile, KW wavefronts splitting K (WM * WN * KW == 4).  KPW > 0 (decode shape):
+// every wavefront owns exactly KPW k-steps and issues all of its loads -- A
+// rows first (L2), then its weights (HBM) -- before the first MFMA, so a
+// launch keeps its whole weight slice in flight at once.  KPW == 0 (prefill
+// shape): a loop over the k-steps, four per iteration.
+template <int MT, int NT, int WM, int WN, int KW, int KPW, bool BF, int EPI, bool NORM, bool AROW = false>
 __global__ __launch_bounds__(NTHR) void gemm_kernel(const GemmArgs g) {
     static_assert(WM * WN * KW == 4, "four wavefronts");
     constexpr int BM = 16 * MT * WM, BN = 16 * NT * WN;
     constexpr int LDR = BN + 1;
-    constexpr int U = 4;                                   // k-steps per loop iteration
+    constexpr int U = 4;                                   // k-steps per loop iteration (prefill shape)
     __shared__ float red[KW][BM][LDR];
     __shared__ float ssl[KW][BM];
     __shared__ int s_flag;
     __shared__ unsigned s_tag;
 
-    if (step_done(g.st)) return;
+    // decode shape: nothing waits on the step state before the main loads are
+    // in flight (a launch after the done flag computes and stores nothing)
+    constexpr bool DEC = KPW > 0;
+    int done_flag = 0;
+    if constexpr (!DEC) {
+        if (step_done(g.st)) return;
+    } else {
+        done_flag = __builtin_nontemporal_load(&g.st->done);
+    }
     const int tid = threadIdx.x, lane = tid & 63;
     const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int kw = w % KW, wn = (w / KW) % WN, wm = w / (KW * WN);
     const int tile_n = blockIdx.x / g.ks, ksi = blockIdx.x - tile_n * g.ks, tile_m = blockIdx.y;
-    const int ntn = (g.N + BN - 1) / BN;
     const int r16 = lane & 15, q4 = lane >> 4;
     if (tid == 0) s_tag = __builtin_nontemporal_load(&g.st->tag);
 
@@ -139,7 +151,9 @@ __global__ __launch_bounds__(NTHR) void gemm_kernel(const GemmArgs g) {
     for (int mt = 0; mt < MT; mt++) {
         const int m = tile_m * BM + wm * 16 * MT + 16 * mt + r16;
         int pm = m;
-        if (g.arow) pm = g.arow[m < g.M ? m : 0];
+        // a row map only where one is used (a possible load here would make
+        // every later wait cover it)
+        if (AROW) pm = g.arow[m < g.M ? m : 0];
         aoff[mt] = (unsigned)(((size_t)pm * g.lda + 4 * q4) * 4);
     }
 #pragma unroll
@@ -157,35 +171,98 @@ __global__ __launch_bounds__(NTHR) void gemm_kernel(const GemmArgs g) {
 #pragma unroll
     for (int mt = 0; mt < MT; mt++) ss[mt] = 0.f;
 
-    for (int kb = kb0; kb < kb1; kb += U) {
-        f4 a[U][MT], b[U][NT], gm[U];
+    auto kstep = [&](f4 (&a)[MT], const f4 (&b)[NT], const f4 &gm) {
+        if (NORM) {
 #pragma unroll
-        for (int u = 0; u < U; u++) {
-#pragma unroll
-            for (int nt = 0; nt < NT; nt++) b[u][nt] = ldw4<BF>(rw, woff[nt] + (unsigned)((kb + u) * 16));
-#pragma unroll
-            for (int mt = 0; mt < MT; mt++) a[u][mt] = lda4(ra, aoff[mt] + (unsigned)((kb + u) * 64));
-            if (NORM) gm[u] = lda4(rg, (unsigned)(((kb + u) * 16 + 4 * q4) * 4));
+            for (int mt = 0; mt < MT; mt++) {
+                f4 &x = a[mt];
+                ss[mt] += x.x * x.x + x.y * x.y + x.z * x.z + x.w * x.w;
+                x.x *= gm.x; x.y *= gm.y; x.z *= gm.z; x.w *= gm.w;
+            }
         }
 #pragma unroll
-        for (int u = 0; u < U; u++) {
-            if (NORM) {
+        for (int mt = 0; mt < MT; mt++)
 #pragma unroll
-                for (int mt = 0; mt < MT; mt++) {
-                    f4 &x = a[u][mt];
-                    ss[mt] += x.x * x.x + x.y * x.y + x.z * x.z + x.w * x.w;
-                    x.x *= gm[u].x; x.y *= gm[u].y; x.z *= gm[u].z; x.w *= gm[u].w;
-                }
+            for (int nt = 0; nt < NT; nt++) {
+                acc[mt][nt] = mfma4(a[mt].x, b[nt].x, acc[mt][nt]);
+                acc[mt][nt] = mfma4(a[mt].y, b[nt].y, acc[mt][nt]);
+                acc[mt][nt] = mfma4(a[mt].z, b[nt].z, acc[mt][nt]);
+                acc[mt][nt] = mfma4(a[mt].w, b[nt].w, acc[mt][nt]);
+            }
+    };
+
+    // decode shape: the epilogue's operands of this thread's column pairs,
+    // loaded before the main loads so that they arrive with them
+    constexpr int EP = DEC ? (BM * BN / 2 + NTHR - 1) / NTHR : 1;
+    float eb0[EP], eb1[EP], er0[EP], er1[EP], ecs[EP], esn[EP];
+    int erb[EP], erp[EP];
+    if constexpr (DEC) {
+#pragma unroll
+        for (int e = 0; e < EP; e++) {
+            const int i = tid + e * NTHR;
+            const int m = i / (BN / 2), n = 2 * (i - m * (BN / 2));
+            const int gm_ = tile_m * BM + m, gn = tile_n * BN + n;
+            eb0[e] = eb1[e] = er0[e] = er1[e] = ecs[e] = esn[e] = 0.f;
+            erb[e] = erp[e] = 0;
+            if (i >= BM * BN / 2 || gm_ >= g.M || gn >= g.N) continue;
+            if (EPI == EPI_SWIGLU) { eb0[e] = g.bias[gn >> 1]; eb1[e] = g.bias2[gn >> 1]; }
+            else { eb0[e] = g.bias[gn]; eb1[e] = g.bias[gn + 1]; }
+            if (EPI == EPI_RES) { er0[e] = g.res[(size_t)gm_ * g.ldr + gn]; er1[e] = g.res[(size_t)gm_ * g.ldr + gn + 1]; }
+            if (EPI == EPI_QKV) { erb[e] = g.row_b[gm_]; erp[e] = g.row_p[gm_]; }
+        }
+    }
+
+    if constexpr (KPW > 0) {
+        f4 a[KPW][MT], b[KPW][NT], gm[KPW];
+#pragma unroll
+        for (int u = 0; u < KPW; u++) {
+#pragma unroll
+            for (int mt = 0; mt < MT; mt++) a[u][mt] = lda4(ra, aoff[mt] + (unsigned)((kb0 + u) * 64));
+            if (NORM) gm[u] = lda4(rg, (unsigned)(((kb0 + u) * 16 + 4 * q4) * 4));
+        }
+#pragma unroll
+        for (int u = 0; u < KPW; u++)
+#pragma unroll
+            for (int nt = 0; nt < NT; nt++) b[u][nt] = ldw4<BF>(rw, woff[nt] + (unsigned)((kb0 + u) * 16));
+        // the RoPE loads wait for their positions: issue them only after every
+        // main load is in flight (the empty asm keeps the compiler from
+        // computing with the rows' positions before this point)
+        __builtin_amdgcn_sched_barrier(0);
+        if (EPI == EPI_QKV) {
+#pragma unroll
+            for (int e = 0; e < EP; e++) asm volatile("" : "+v"(erb[e]), "+v"(erp[e]));
+        }
+        if (EPI == EPI_QKV && g.rope) {
+            // RoPE entries of this thread's rows (their positions arrived first)
+#pragma unroll
+            for (int e = 0; e < EP; e++) {
+                const int i = tid + e * NTHR;
+                const int m = i / (BN / 2), n = 2 * (i - m * (BN / 2));
+                const int gm_ = tile_m * BM + m, gn = tile_n * BN + n;
+                if (i >= BM * BN / 2 || gm_ >= g.M || gn >= 2 * g.D) continue;
+                const int d = (gn % g.D) % BK_DK;
+                ecs[e] = g.rope[(size_t)erp[e] * (BK_DK / 2) + d / 2];
+                esn[e] = g.rope[(size_t)(g.rope_rows + erp[e]) * (BK_DK / 2) + d / 2];
+            }
+        }
+        // keep every load above the first MFMA (the scheduler would otherwise
+        // sink loads towards their uses and serialise the HBM round trips)
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int u = 0; u < KPW; u++) kstep(a[u], b[u], gm[u]);
+    } else {
+        for (int kb = kb0; kb < kb1; kb += U) {
+            f4 a[U][MT], b[U][NT], gm[U];
+#pragma unroll
+            for (int u = 0; u < U; u++) {
+#pragma unroll
+                for (int nt = 0; nt < NT; nt++) b[u][nt] = ldw4<BF>(rw, woff[nt] + (unsigned)((kb + u) * 16));
+#pragma unroll
+                for (int mt = 0; mt < MT; mt++) a[u][mt] = lda4(ra, aoff[mt] + (unsigned)((kb + u) * 64));
+                if (NORM) gm[u] = lda4(rg, (unsigned)(((kb + u) * 16 + 4 * q4) * 4));
             }
 #pragma unroll
-            for (int mt = 0; mt < MT; mt++)
-#pragma unroll
-                for (int nt = 0; nt < NT; nt++) {
-                    acc[mt][nt] = mfma4(a[u][mt].x, b[u][nt].x, acc[mt][nt]);
-                    acc[mt][nt] = mfma4(a[u][mt].y, b[u][nt].y, acc[mt][nt]);
-                    acc[mt][nt] = mfma4(a[u][mt].z, b[u][nt].z, acc[mt][nt]);
-                    acc[mt][nt] = mfma4(a[u][mt].w, b[u][nt].w, acc[mt][nt]);
-                }
+            for (int u = 0; u < U; u++) kstep(a[u], b[u], gm[u]);
         }
     }
 
@@ -203,19 +280,21 @@ __global__ __launch_bounds__(NTHR) void gemm_kernel(const GemmArgs g) {
     if (NORM) {
 #pragma unroll
         for (int mt = 0; mt < MT; mt++) {
-            float s = ss[mt];
-            s += __shfl_xor(s, 16);
-            s += __shfl_xor(s, 32);
-            if (wn == 0 && q4 == 0) ssl[kw][wm * 16 * MT + 16 * mt + r16] = s;
+            float sv = ss[mt];
+            sv += __shfl_xor(sv, 16);
+            sv += __shfl_xor(sv, 32);
+            if (wn == 0 && q4 == 0) ssl[kw][wm * 16 * MT + 16 * mt + r16] = sv;
         }
     }
     __syncthreads();
+    if (DEC && done_flag) return;
     const unsigned tag = s_tag * 128u + (unsigned)g.kslot;
 
-    // split K over workgroups: publish the partial tile, the last to arrive sums
-    // all partials in workgroup order (a fixed order: the result does not
-    // depend on which one arrives last)
-    const rsrc_t rp = buf(g.part, g.part ? (size_t)g.ks * g.M * g.N * 8 : 0);
+    // split K over workgroups: publish the partial tile (and the rows' partial
+    // sums of squares), the last to arrive sums all partials in workgroup
+    // order (a fixed order: the result does not depend on which one arrives last)
+    const size_t n_main = (size_t)g.ks * g.M * g.N;
+    const rsrc_t rp = buf(g.part, g.part ? (n_main + (size_t)gridDim.x * g.M) * 8 : 0);
     if (g.ks > 1) {
         for (int i = tid; i < BM * BN / 2; i += NTHR) {
             const int m = i / (BN / 2), n = 2 * (i - m * (BN / 2));
@@ -226,58 +305,103 @@ __global__ __launch_bounds__(NTHR) void gemm_kernel(const GemmArgs g) {
             for (int k = 0; k < KW; k++) { v0 += red[k][m][n]; v1 += red[k][m][n + 1]; }
             st_pair2(rp, ((size_t)ksi * g.M + gm_) * g.N + gn, v0, v1, tag);
         }
-        if (!arrive_last(g.cnt + tile_n, (unsigned)g.ks, &s_flag)) return;
+        if (NORM)
+            for (int m = tid; m < BM; m += NTHR) {
+                const int gm_ = tile_m * BM + m;
+                if (gm_ >= g.M) continue;
+                float sv = 0.f;
+#pragma unroll
+                for (int k = 0; k < KW; k++) sv += ssl[k][m];
+                put(rp, n_main + ((size_t)tile_n * g.ks + ksi) * g.M + gm_, sv, tag);
+            }
+        if (!arrive_last(g.cnt + tile_m * (gridDim.x / g.ks) + tile_n, (unsigned)g.ks, &s_flag)) return;
+        if (NORM) {
+            // the rows' sums of squares over all K, into ssl[0]
+            for (int m = tid; m < BM; m += NTHR) {
+                const int gm_ = tile_m * BM + m;
+                if (gm_ >= g.M) continue;
+                float sv = 0.f;
+                for (int k = 0; k < g.ks; k++) {
+                    const size_t pr = n_main + ((size_t)tile_n * g.ks + k) * g.M + gm_;
+                    u2 p = __builtin_bit_cast(u2, __builtin_amdgcn_raw_buffer_load_b64(rp, (unsigned)(pr * 8), 0, CP_SC1));
+                    for (unsigned spin = 0; p.y != tag && spin < SPIN_CAP; spin++) {
+                        __builtin_amdgcn_s_sleep(1);
+                        p = __builtin_bit_cast(u2, __builtin_amdgcn_raw_buffer_load_b64(rp, (unsigned)(pr * 8), 0, CP_SC1));
+                    }
+                    sv += as_float(p.x);
+                }
+                ssl[0][m] = sv;
+            }
+            __syncthreads();
+        }
     }
 
     // epilogue: two adjacent columns per thread
-    for (int i = tid; i < BM * BN / 2; i += NTHR) {
+#pragma unroll
+    for (int e = 0; e < (DEC ? EP : 1); e++)
+    for (int i = tid + e * NTHR; i < BM * BN / 2; i += (DEC ? BM * BN : NTHR)) {
         const int m = i / (BN / 2), n = 2 * (i - m * (BN / 2));
         const int gm_ = tile_m * BM + m, gn = tile_n * BN + n;
         if (gm_ >= g.M || gn >= g.N) continue;
         float v0 = 0.f, v1 = 0.f;
         if (g.ks > 1) {
-            for (int k = 0; k < g.ks; k++) {
-                u4 p = ld_pair2(rp, ((size_t)k * g.M + gm_) * g.N + gn);
-                for (unsigned spin = 0; (p.y != tag || p.w != tag) && spin < SPIN_CAP; spin++) {
+            // issue every partial's load, then check the tags (re-poll only a
+            // partial that is not yet visible)
+            constexpr int KSMAX = 8;
+            u4 p[KSMAX];
+#pragma unroll
+            for (int k = 0; k < KSMAX; k++)
+                if (k < g.ks) p[k] = ld_pair2(rp, ((size_t)k * g.M + gm_) * g.N + gn);
+#pragma unroll
+            for (int k = 0; k < KSMAX; k++) {
+                if (k >= g.ks) break;
+                for (unsigned spin = 0; (p[k].y != tag || p[k].w != tag) && spin < SPIN_CAP; spin++) {
                     __builtin_amdgcn_s_sleep(1);
-                    p = ld_pair2(rp, ((size_t)k * g.M + gm_) * g.N + gn);
+                    p[k] = ld_pair2(rp, ((size_t)k * g.M + gm_) * g.N + gn);
                 }
-                v0 += as_float(p.x);
-                v1 += as_float(p.z);
+                v0 += as_float(p[k].x);
+                v1 += as_float(p[k].z);
             }
         } else {
 #pragma unroll
             for (int k = 0; k < KW; k++) { v0 += red[k][m][n]; v1 += red[k][m][n + 1]; }
         }
         if (NORM) {
-            float s = 0.f;
+            float sv = 0.f;
+            if (g.ks > 1) sv = ssl[0][m];
+            else {
 #pragma unroll
-            for (int k = 0; k < KW; k++) s += ssl[k][m];
-            const float rs = 1.0f / sqrtf(s * (1.0f / (float)g.dnorm) + g.eps);
+                for (int k = 0; k < KW; k++) sv += ssl[k][m];
+            }
+            const float rs = 1.0f / sqrtf(sv * (1.0f / (float)g.dnorm) + g.eps);
             v0 *= rs;
             v1 *= rs;
         }
+        // the epilogue's operands: prefetched (decode shape) or loaded here
+        const bool pf = DEC;
+        const int ei = DEC ? e : 0;
         if (EPI == EPI_RES) {
-            const float y0 = v0 + g.bias[gn], y1 = v1 + g.bias[gn + 1];
-            const float *rr = g.res + (size_t)gm_ * g.ldr + gn;
+            const float y0 = v0 + (pf ? eb0[ei] : g.bias[gn]), y1 = v1 + (pf ? eb1[ei] : g.bias[gn + 1]);
+            const float r0 = pf ? er0[ei] : g.res[(size_t)gm_ * g.ldr + gn];
+            const float r1 = pf ? er1[ei] : g.res[(size_t)gm_ * g.ldr + gn + 1];
             float *o = g.out + (size_t)gm_ * g.ldo + gn;
-            o[0] = rr[0] + y0;
-            o[1] = rr[1] + y1;
+            o[0] = r0 + y0;
+            o[1] = r1 + y1;
         } else if (EPI == EPI_SWIGLU) {
             // rows 2f (gate) and 2f+1 (up) of the interleaved gate/up matrix
             const int f = gn >> 1;
-            const float gt = v0 + g.bias[f], up = v1 + g.bias2[f];
+            const float gt = v0 + (pf ? eb0[ei] : g.bias[f]), up = v1 + (pf ? eb1[ei] : g.bias2[f]);
             g.out[(size_t)gm_ * g.ldo + f] = (gt / (1.0f + expf(-gt))) * up;
         } else if (EPI == EPI_QKV) {
-            float y0 = v0 + g.bias[gn], y1 = v1 + g.bias[gn + 1];
+            float y0 = v0 + (pf ? eb0[ei] : g.bias[gn]), y1 = v1 + (pf ? eb1[ei] : g.bias[gn + 1]);
             const int sec = gn / g.D, c = gn - sec * g.D, h = c / BK_DK, d = c - h * BK_DK;
-            const int b = g.row_b[gm_], p = g.row_p[gm_];
+            const int b = pf ? erb[ei] : g.row_b[gm_], p = pf ? erp[ei] : g.row_p[gm_];
             if (sec < 2 && g.rope) {
-                const float cs = g.rope[(size_t)p * (BK_DK / 2) + d / 2];
-                const float sn = g.rope[(size_t)(g.rope_rows + p) * (BK_DK / 2) + d / 2];
-                const float e = y0, o = y1;
-                y0 = e * cs - o * sn;
-                y1 = e * sn + o * cs;
+                const float cs = pf ? ecs[ei] : g.rope[(size_t)p * (BK_DK / 2) + d / 2];
+                const float sn = pf ? esn[ei] : g.rope[(size_t)(g.rope_rows + p) * (BK_DK / 2) + d / 2];
+                const float e0 = y0, o0 = y1;
+                y0 = e0 * cs - o0 * sn;
+                y1 = e0 * sn + o0 * cs;
             }
             const size_t head = (((size_t)g.layer * g.B + b) * g.H + h) * (size_t)BK_DK * g.kv_s;
             if (sec == 0) {
@@ -291,7 +415,7 @@ __global__ __launch_bounds__(NTHR) void gemm_kernel(const GemmArgs g) {
                 g.vc[head + (size_t)p * BK_DK + d + 1] = y1;
             }
         } else {   // EPI_HEAD: logits into the LDS tile for the argmax pass
-            const float y0 = v0 + g.bias[gn], y1 = v1 + g.bias[gn + 1];
+            const float y0 = v0 + (pf ? eb0[ei] : g.bias[gn]), y1 = v1 + (pf ? eb1[ei] : g.bias[gn + 1]);
             red[0][m][n] = y0;
             red[0][m][n + 1] = y1;
             if (g.logits) {
@@ -301,75 +425,127 @@ __global__ __launch_bounds__(NTHR) void gemm_kernel(const GemmArgs g) {
             }
         }
     }
-    if (EPI != EPI_HEAD) return;
-
-    // ---- argmax of this tile's columns per row, then the last workgroup of
-    // the launch reduces the tiles and feeds the next step
-    __syncthreads();
-    const rsrc_t rx = buf(g.amax, (size_t)g.M * ntn * 8);
-    for (int m = tid; m < BM; m += NTHR) {
-        const int gm_ = tile_m * BM + m;
-        if (gm_ >= g.M) continue;
-        float best = -INFINITY;
-        int bi = tile_n * BN;
-        for (int n = 0; n < BN; n++) {
-            const int gn = tile_n * BN + n;
-            if (gn < g.N && red[0][m][n] > best) { best = red[0][m][n]; bi = gn; }
-        }
-        const u2 pr = {as_uint(best), (unsigned)bi | (s_tag << 16)};
-        __builtin_amdgcn_raw_buffer_store_b64(pr, rx, (unsigned)(((size_t)gm_ * ntn + tile_n) * 8), 0, CP_SC1);
-    }
-    if (!arrive_last(g.head_cnt, (unsigned)(ntn * gridDim.y), &s_flag)) return;
-
-    // ---- the last workgroup: one wavefront per row
-    const int t = g.prefill ? 0 : g.st->t;
-    const unsigned tag16 = s_tag & 0xffffu;
-    for (int m = w; m < g.M; m += NTHR / 64) {
-        float best = -INFINITY;
-        int bi = 0x7fffffff;
-        for (int tn = lane; tn < ntn; tn += 64) {
-            u2 p = __builtin_bit_cast(u2, __builtin_amdgcn_raw_buffer_load_b64(rx, (unsigned)(((size_t)m * ntn + tn) * 8), 0, CP_SC1));
-            for (unsigned spin = 0; (p.y >> 16) != tag16 && spin < SPIN_CAP; spin++) {
-                __builtin_amdgcn_s_sleep(1);
-                p = __builtin_bit_cast(u2, __builtin_amdgcn_raw_buffer_load_b64(rx, (unsigned)(((size_t)m * ntn + tn) * 8), 0, CP_SC1));
+    if constexpr (EPI == EPI_HEAD) {
+        // argmax of this tile's columns per row (first index of the maximum);
+        // head_finish_kernel reduces the tiles after this launch
+        __syncthreads();
+        const int ntn = (g.N + BN - 1) / BN;
+        for (int m = tid; m < BM; m += NTHR) {
+            const int gm_ = tile_m * BM + m;
+            if (gm_ >= g.M) continue;
+            float best = -INFINITY;
+            int bi = tile_n * BN;
+            for (int n = 0; n < BN; n++) {
+                const int gn = tile_n * BN + n;
+                if (gn < g.N && red[0][m][n] > best) { best = red[0][m][n]; bi = gn; }
             }
-            const float v = as_float(p.x);
-            const int idx = (int)(p.y & 0xffffu);
-            if (v > best || (v == best && idx < bi)) { best = v; bi = idx; }
+            g.amax[(size_t)gm_ * ntn + tile_n] = make_uint2(as_uint(best), (unsigned)bi);
         }
-        // wavefront reduction: larger value, then lower index
+    }
+}
+
+// The lm_head's argmax over its column tiles (gpt.c:220-230: the first index of
+// the maximum), then the step's bookkeeping: one workgroup of FIN_THR threads,
+// wavefront w taking rows w, w + 16, ...; the step state, each row's feed and
+// the tiles' partials are loaded together up front.
+constexpr int FIN_THR = 1024;
+constexpr int FIN_ROWS = BK_MAXM / (FIN_THR / 64);     // rows per wavefront
+__global__ __launch_bounds__(FIN_THR) void head_finish_kernel(const GemmArgs g) {
+    __shared__ int s_done[BK_MAXM];
+    const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+    const int done = __builtin_nontemporal_load(&g.st->done);
+    const int t = g.prefill ? 0 : g.st->t;
+    const int ntn = g.amax_tiles;
+    if (tid < BK_MAXM) s_done[tid] = 0;
+    int nf[FIN_ROWS];
+    float best[FIN_ROWS];
+    int bi[FIN_ROWS];
+#pragma unroll
+    for (int r = 0; r < FIN_ROWS; r++) {
+        best[r] = -INFINITY;
+        bi[r] = 0x7fffffff;
+        const int m = w + 16 * r;
+        nf[r] = (!g.prefill && m < g.M) ? g.n_feed[m] : 0;
+    }
+    // the partials in passes of FIN_PASS tiles per lane, every load of a pass
+    // (all rows of the wavefront) issued before the first compare; tiles in
+    // increasing order per lane, strict '>' keeps the first maximum
+    constexpr int FIN_PASS = 8;
+    for (int t0 = 0; t0 < ntn; t0 += 64 * FIN_PASS) {
+        uint2 pv[FIN_ROWS][FIN_PASS];
+#pragma unroll
+        for (int r = 0; r < FIN_ROWS; r++)
+#pragma unroll
+            for (int j = 0; j < FIN_PASS; j++) {
+                const int m = w + 16 * r, tn = t0 + lane + 64 * j;
+                pv[r][j] = (m < g.M && tn < ntn) ? g.amax[(size_t)m * ntn + tn] : make_uint2(as_uint(-INFINITY), 0x7fffffffu);
+            }
+#pragma unroll
+        for (int r = 0; r < FIN_ROWS; r++)
+#pragma unroll
+            for (int j = 0; j < FIN_PASS; j++) {
+                const float v = as_float(pv[r][j].x);
+                const int idx = (int)pv[r][j].y;
+                if (v > best[r] || (v == best[r] && idx < bi[r])) { best[r] = v; bi[r] = idx; }
+            }
+    }
+    if (done) return;
+    __syncthreads();
+#pragma unroll
+    for (int r = 0; r < FIN_ROWS; r++) {
+        const int m = w + 16 * r;
+        if (m >= g.M) continue;
+        float bv = best[r];
+        int bx = bi[r];
 #pragma unroll
         for (int o = 32; o >= 1; o >>= 1) {
-            const float ov = __shfl_xor(best, o);
-            const int oi = __shfl_xor(bi, o);
-            if (ov > best || (ov == best && oi < bi)) { best = ov; bi = oi; }
+            const float ov = __shfl_xor(bv, o);
+            const int oi = __shfl_xor(bx, o);
+            if (ov > bv || (ov == bv && oi < bx)) { bv = ov; bx = oi; }
         }
-        if (bi == 0x7fffffff) bi = 0;
-        const int tok = bi;
+        const int tok = bx == 0x7fffffff ? 0 : bx;
         if (g.prefill) {
             if (lane == 0) g.ids[m] = tok;
             continue;
         }
+        const bool greedy = t >= nf[r] - 1;
         if (lane == 0) {
             g.ids[(size_t)t * g.M + m] = tok;
-            if (g.eos >= 0 && t >= g.n_feed[m] - 1 && tok == g.eos) g.row_done[m] = 1;
+            s_done[m] = g.eos >= 0 && greedy && tok == g.eos;
             g.pos[m] += 1;
         }
-        const int nxt = (t + 1 < g.n_feed[m]) ? g.feed[(size_t)(t + 1) * g.M + m] : tok;
+        // the next step's embedding row (embedding.c:79-84): every load of the
+        // row before the first store (a store may alias a later load, which
+        // would otherwise serialise the copy)
+        const int nxt = (t + 1 < nf[r]) ? g.feed[(size_t)(t + 1) * g.M + m] : tok;
         const float *e = g.embed + (size_t)nxt * g.ldx;
         float *x = g.x_next + (size_t)m * g.ldx;
-        for (int c = lane; c < g.D; c += 64) x[c] = e[c];
+        constexpr int CPL = BK_MAXD / 64;
+        float ev[CPL];
+#pragma unroll
+        for (int j = 0; j < CPL; j++) ev[j] = (lane + 64 * j < g.D) ? e[lane + 64 * j] : 0.f;
+#pragma unroll
+        for (int j = 0; j < CPL; j++)
+            if (lane + 64 * j < g.D) x[lane + 64 * j] = ev[j];
+    }
+    __syncthreads();
+    // rows that stopped in an earlier step stay stopped; one thread per row
+    __shared__ int s_all;
+    if (tid == 0) s_all = g.eos >= 0;
+    __syncthreads();
+    if (!g.prefill && tid < g.M) {
+        const int dr = s_done[tid] | g.row_done[tid];
+        g.row_done[tid] = dr;
+        if (!dr) s_all = 0;
     }
     __syncthreads();
     if (tid == 0) {
         if (!g.prefill) {
-            int all = g.eos >= 0;
-            for (int m = 0; m < g.M; m++) all &= g.row_done[m];
             g.st->t = t + 1;
             *g.steps_done = t + 1;
-            if (all) g.st->done = 1;
+            if (s_all) g.st->done = 1;
         }
-        g.st->tag = s_tag + 1;
+        g.st->tag = g.st->tag + 1;
     }
 }
 
@@ -381,41 +557,52 @@ __global__ __launch_bounds__(NTHR) void gemm_kernel(const GemmArgs g) {
 // and dims 4(l%16) + 0..3 of keys 64c + l/16 + 4i for P.V.  Running max /
 // sum per wavefront (transformer.c:354-359), merged across wavefronts in LDS
 // and across splits by the last workgroup of the (row, head).
-__global__ __launch_bounds__(NTHR) void attn_kernel(const AttnArgs a) {
-    __shared__ float s_p[4][64];
-    __shared__ float s_o[4][BK_DK];
-    __shared__ float s_ml[4][2];
+__global__ __launch_bounds__(ATHR) void attn_kernel(const AttnArgs a) {
+    constexpr int AW = ATHR / 64;                     // wavefronts
+    __shared__ float s_p[AW][64];
+    __shared__ float s_o[AW][BK_DK];
+    __shared__ float s_ml[AW][2];
     __shared__ int s_flag;
     __shared__ unsigned s_tag;
-    if (step_done(a.st)) return;
     const int tid = threadIdx.x, lane = tid & 63;
     const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int bh = blockIdx.x / a.nsplit, sp = blockIdx.x - bh * a.nsplit;
     const int m = bh / a.H, h = bh - m * a.H;
     if (tid == 0) s_tag = __builtin_nontemporal_load(&a.st->tag);
-    const int S = a.pos[m] + 1;
-    const int nch = (S + 63) / 64;
     const int r16 = lane & 15, q4 = lane >> 4;
     const size_t head = (((size_t)a.layer * a.B + m) * a.H + h) * (size_t)BK_DK * a.kv_s;
     const rsrc_t rk = buf(a.kc + head, (size_t)BK_DK * a.kv_s * 4);
     const rsrc_t rv = buf(a.vc + head, (size_t)BK_DK * a.kv_s * 4);
+    // the step state, the row's length, its query and this wavefront's first
+    // chunk of keys and values, all in flight together (the chunk is loaded
+    // before the length is known: the descriptor bounds it to the row's cache)
+    const int done = __builtin_nontemporal_load(&a.st->done);
+    const int posm = a.pos[m];
     float qv[16];
 #pragma unroll
     for (int i = 0; i < 16; i++) qv[i] = a.q[(size_t)m * a.D + h * BK_DK + q4 + 4 * i];
-
-    float mrun = -INFINITY, lrun = 0.f;
-    f4 o = {0.f, 0.f, 0.f, 0.f};
-    for (int c = sp + a.nsplit * w; c < nch; c += 4 * a.nsplit) {
+    const int c0 = sp + a.nsplit * w;
+    f4 kt[16], vv[16];
+    auto load_chunk = [&](int c) {
         const int j0 = 64 * c;
-        // scores of keys j0 + 4 r16 + 0..3
-        f4 kt[16];
 #pragma unroll
         for (int i = 0; i < 16; i++)
             kt[i] = lda4(rk, (unsigned)((((size_t)(q4 + 4 * i)) * a.kv_s + j0 + 4 * r16) * 4));
-        f4 vv[16];
 #pragma unroll
         for (int i = 0; i < 16; i++)
             vv[i] = lda4(rv, (unsigned)((((size_t)(j0 + q4 + 4 * i)) * BK_DK + 4 * r16) * 4));
+    };
+    load_chunk(c0);
+    __builtin_amdgcn_sched_barrier(0);
+    if (done) return;
+    const int S = posm + 1;
+    const int nch = (S + 63) / 64;
+
+    float mrun = -INFINITY, lrun = 0.f;
+    f4 o = {0.f, 0.f, 0.f, 0.f};
+    for (int c = c0; c < nch; c += AW * a.nsplit) {
+        const int j0 = 64 * c;
+        if (c != c0) load_chunk(c);
         f4 s = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
         for (int i = 0; i < 16; i++) {
@@ -462,12 +649,12 @@ __global__ __launch_bounds__(NTHR) void attn_kernel(const AttnArgs a) {
     if (q4 == 0) *reinterpret_cast<f4 *>(&s_o[w][4 * r16]) = o;
     if (lane == 0) { s_ml[w][0] = mrun; s_ml[w][1] = lrun; }
     __syncthreads();
-    // merge the four wavefronts: thread d < 64 owns output dim d
+    // merge the wavefronts: thread d < 64 owns output dim d
     float om = -INFINITY;
-    for (int k = 0; k < 4; k++) om = fmaxf(om, s_ml[k][0]);
+    for (int k = 0; k < AW; k++) om = fmaxf(om, s_ml[k][0]);
     float ol = 0.f, od = 0.f;
     if (tid < BK_DK) {
-        for (int k = 0; k < 4; k++) {
+        for (int k = 0; k < AW; k++) {
             if (s_ml[k][0] == -INFINITY) continue;
             const float f = expf(s_ml[k][0] - om);
             ol += s_ml[k][1] * f;
@@ -487,24 +674,42 @@ __global__ __launch_bounds__(NTHR) void attn_kernel(const AttnArgs a) {
     if (tid == 0) { put(rp, rec * (BK_DK + 2) + BK_DK, om, tag); put(rp, rec * (BK_DK + 2) + BK_DK + 1, ol, tag); }
     if (!arrive_last(a.cnt + bh, (unsigned)a.nsplit, &s_flag)) return;
     if (tid >= BK_DK) return;
-    auto get = [&](size_t pr) {
-        u2 v = __builtin_bit_cast(u2, __builtin_amdgcn_raw_buffer_load_b64(rp, (unsigned)(pr * 8), 0, CP_SC1));
+    // every split's (m, l, o[tid]) loaded at once, tags checked afterwards
+    constexpr int NSMAX = 8;
+    u2 pm[NSMAX], pl[NSMAX], po[NSMAX];
+#pragma unroll
+    for (int k = 0; k < NSMAX; k++) {
+        if (k >= a.nsplit) break;
+        const size_t r = ((size_t)bh * a.nsplit + k) * (BK_DK + 2);
+        pm[k] = __builtin_bit_cast(u2, __builtin_amdgcn_raw_buffer_load_b64(rp, (unsigned)((r + BK_DK) * 8), 0, CP_SC1));
+        pl[k] = __builtin_bit_cast(u2, __builtin_amdgcn_raw_buffer_load_b64(rp, (unsigned)((r + BK_DK + 1) * 8), 0, CP_SC1));
+        po[k] = __builtin_bit_cast(u2, __builtin_amdgcn_raw_buffer_load_b64(rp, (unsigned)((r + tid) * 8), 0, CP_SC1));
+    }
+    auto settle = [&](u2 &v, size_t pr) {
         for (unsigned spin = 0; v.y != tag && spin < SPIN_CAP; spin++) {
             __builtin_amdgcn_s_sleep(1);
             v = __builtin_bit_cast(u2, __builtin_amdgcn_raw_buffer_load_b64(rp, (unsigned)(pr * 8), 0, CP_SC1));
         }
-        return as_float(v.x);
     };
     float gm = -INFINITY;
-    for (int k = 0; k < a.nsplit; k++) gm = fmaxf(gm, get(((size_t)bh * a.nsplit + k) * (BK_DK + 2) + BK_DK));
-    float gl = 0.f, gd = 0.f;
-    for (int k = 0; k < a.nsplit; k++) {
+#pragma unroll
+    for (int k = 0; k < NSMAX; k++) {
+        if (k >= a.nsplit) break;
         const size_t r = ((size_t)bh * a.nsplit + k) * (BK_DK + 2);
-        const float km = get(r + BK_DK);
+        settle(pm[k], r + BK_DK);
+        settle(pl[k], r + BK_DK + 1);
+        settle(po[k], r + tid);
+        gm = fmaxf(gm, as_float(pm[k].x));
+    }
+    float gl = 0.f, gd = 0.f;
+#pragma unroll
+    for (int k = 0; k < NSMAX; k++) {
+        if (k >= a.nsplit) break;
+        const float km = as_float(pm[k].x);
         if (km == -INFINITY) continue;
         const float f = expf(km - gm);
-        gl += get(r + BK_DK + 1) * f;
-        gd += get(r + tid) * f;
+        gl += as_float(pl[k].x) * f;
+        gd += as_float(po[k].x) * f;
     }
     a.att[(size_t)m * a.ldatt + h * BK_DK + tid] = gd / gl;
 }
@@ -657,24 +862,47 @@ __global__ __launch_bounds__(NTHR) void embed_kernel(const EmbedArgs a) {
 
 namespace {
 
+// decode shape: all rows in one tile (MT = rows / 16), k-steps per wavefront
+// KPW = K / 16 / (4 * ks), chosen by the host among the instantiated values
+template <int EPI, bool NORM, bool BF, int MT>
+hipError_t gemm_decode_mt(const GemmArgs &g, hipStream_t st, int kpw) {
+    const int ntn = (g.N + 15) / 16;
+    dim3 grid(ntn * g.ks, (g.M + 16 * MT - 1) / (16 * MT));
+#define DNNHIP_KPW(K)                                                                                            \
+    case K:                                                                                                      \
+        if (EPI == EPI_HEAD && g.arow)                                                                           \
+            hipLaunchKernelGGL((gemm_kernel<MT, 1, 1, 1, 4, K, BF, EPI, NORM, EPI == EPI_HEAD>), grid, dim3(NTHR), 0, st, g); \
+        else                                                                                                     \
+            hipLaunchKernelGGL((gemm_kernel<MT, 1, 1, 1, 4, K, BF, EPI, NORM>), grid, dim3(NTHR), 0, st, g);     \
+        break;
+    switch (kpw) {
+        DNNHIP_KPW(2) DNNHIP_KPW(3) DNNHIP_KPW(4) DNNHIP_KPW(6) DNNHIP_KPW(8) DNNHIP_KPW(12)
+        default: return hipErrorInvalidValue;
+    }
+#undef DNNHIP_KPW
+    return hipGetLastError();
+}
+
 template <int EPI, bool NORM, bool BF>
 hipError_t gemm_decode(const GemmArgs &g, hipStream_t st) {
-    const int ntn = (g.N + 15) / 16;
-    dim3 grid(ntn * g.ks, 1);
-    const int mt = (g.M + 15) / 16;
+    const int nks = g.K / 16;
+    if (nks % (4 * g.ks)) return hipErrorInvalidValue;
+    const int kpw = nks / (4 * g.ks);
+    int mt = (g.M + 15) / 16;
+    if (g.mt_max > 0 && mt > g.mt_max) mt = g.mt_max;     // row tiles per workgroup (the rest: more workgroups)
     switch (mt) {
-        case 1: hipLaunchKernelGGL((gemm_kernel<1, 1, 1, 1, 4, BF, EPI, NORM>), grid, dim3(NTHR), 0, st, g); break;
-        case 2: hipLaunchKernelGGL((gemm_kernel<2, 1, 1, 1, 4, BF, EPI, NORM>), grid, dim3(NTHR), 0, st, g); break;
-        case 3: hipLaunchKernelGGL((gemm_kernel<3, 1, 1, 1, 4, BF, EPI, NORM>), grid, dim3(NTHR), 0, st, g); break;
-        default: hipLaunchKernelGGL((gemm_kernel<4, 1, 1, 1, 4, BF, EPI, NORM>), grid, dim3(NTHR), 0, st, g); break;
+        case 1: return gemm_decode_mt<EPI, NORM, BF, 1>(g, st, kpw);
+        case 2: return gemm_decode_mt<EPI, NORM, BF, 2>(g, st, kpw);
+        case 3: return gemm_decode_mt<EPI, NORM, BF, 3>(g, st, kpw);
+        case 4: return gemm_decode_mt<EPI, NORM, BF, 4>(g, st, kpw);
+        default: return hipErrorInvalidValue;
     }
-    return hipGetLastError();
 }
 
 template <int EPI, bool NORM, bool BF>
 hipError_t gemm_prefill(const GemmArgs &g, hipStream_t st) {
     dim3 grid((g.N + BK_PBN - 1) / BK_PBN * g.ks, (g.M + BK_PBM - 1) / BK_PBM);
-    hipLaunchKernelGGL((gemm_kernel<4, 4, 2, 2, 1, BF, EPI, NORM>), grid, dim3(NTHR), 0, st, g);
+    hipLaunchKernelGGL((gemm_kernel<4, 4, 2, 2, 1, 0, BF, EPI, NORM>), grid, dim3(NTHR), 0, st, g);
     return hipGetLastError();
 }
 
@@ -703,8 +931,14 @@ hipError_t launch_gemm(int epi, bool norm, bool bf16, bool prefill, const GemmAr
     return bf16 ? gemm_any<true>(epi, norm, prefill, g, stream) : gemm_any<false>(epi, norm, prefill, g, stream);
 }
 
+hipError_t launch_head_finish(const GemmArgs &g, hipStream_t stream) {
+    if (g.M > BK_MAXM) return hipErrorInvalidValue;
+    hipLaunchKernelGGL(head_finish_kernel, dim3(1), dim3(FIN_THR), 0, stream, g);
+    return hipGetLastError();
+}
+
 hipError_t launch_attn(const AttnArgs &a, hipStream_t stream) {
-    hipLaunchKernelGGL(attn_kernel, dim3(a.M * a.H * a.nsplit), dim3(NTHR), 0, stream, a);
+    hipLaunchKernelGGL(attn_kernel, dim3(a.M * a.H * a.nsplit), dim3(ATHR), 0, stream, a);
     return hipGetLastError();
 }
 
