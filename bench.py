@@ -33,7 +33,7 @@ CONFIGS = {
     "c3": (8192, 768, 12, 12, 2048, 32, 32),
     "c2b8": (8192, 768, 12, 12, 2048, 32, 8),
 }
-SEED = {"c1": 1, "c2": 2, "c3": 3, "c2b8": 2}
+SEED = {"c1": 1, "c2": 2, "c3": 3, "c2b8": 2, "c4": 4, "c5": 5}
 KERNELS = {3: "decode_v3<NB,DC>", 4: "decode_v4<NB,DC>", 5: "decode_v5<NB,DC>",
            6: "batched engine: gemm_kernel / attn_kernel chain, one HIP graph replay per step"}
 
@@ -65,9 +65,10 @@ def host_lib():
 class DeviceModel:
     """The host library's HBM mirror, shaped like dnn_amd.HipModel for sessions."""
 
-    def __init__(self, ptr, V):
+    def __init__(self, ptr, V, D=0):
         self.ptr = C.c_void_p(ptr)
         self.V = V
+        self.D = D
 
 
 def build_model(L, cfg, max_seq):
@@ -80,7 +81,7 @@ def build_model(L, cfg, max_seq):
     L.decoder_lm_init_normal(lm, 0.02)
     L.decoder_lm_enable_rope(ctx.params, lm, max_seq, 10000.0)
     dm = L.decoder_lm_device_model(lm)
-    return ctx, lm, DeviceModel(dm, V)
+    return ctx, lm, DeviceModel(dm, V, D)
 
 
 def prompts(L, cfg, V, P, B):
@@ -148,71 +149,217 @@ def cpu_baseline(cfg, budget_tokens):
             "kind": "port", "sample": sample + " (oracle/dnn_oracle.c restatement)"}
 
 
+def decode_run(L, cfg, steps, warmup, grid=0):
+    """Greedy decode of CONFIGS[cfg]: prompt, warmup, then exactly `steps` timed
+    steps in one dnn_hip_decode call.  Returns the measurement dict."""
+    V, D, Ly, H, F, P, B = CONFIGS[cfg]
+    max_seq = P + warmup + steps + 1
+    ctx, lm, dm = build_model(L, cfg, max(max_seq, 1088))
+    s = dnn_amd.HipSession(dm, B, max_seq)
+    if grid:
+        s.set_grid(grid)
+    feed = prompts(L, cfg, V, P, B)
+    ids, _ = s.decode(feed, P)                      # prompt, one token per step
+    if warmup:
+        ids, _ = s.decode(ids[-1:], warmup)         # warmup (greedy)
+    start_pos = int(s.lengths()[0])
+    t0 = time.perf_counter()
+    ids, _ = s.decode(ids[-1:], steps)              # timed: exactly `steps` greedy steps
+    wall = time.perf_counter() - t0
+    dev_ms = s.last_ms()
+    assert ids.shape[0] == steps
+    positions = range(start_pos, start_pos + steps)
+    nbytes = step_bytes(V, D, Ly, F, positions, B)
+    achieved = nbytes / (dev_ms * 1e-3) / 1e9
+    kern = s.kernel()
+    return {
+        "tok_s": B * steps / wall, "ms_per_step": wall * 1e3 / steps, "device_ms_per_step": dev_ms / steps,
+        "achieved": achieved, "nbytes": nbytes, "kernel": kern, "grid": s.grid(), "B": B,
+        "positions": [start_pos, start_pos + steps - 1], "P": P,
+        "kernel_desc": ("dnnhip::%s (one persistent launch = %d steps)" % (KERNELS[kern], steps)) if kern in (3, 4, 5)
+        else "dnnhip::%s (%d replays)" % (KERNELS.get(kern, "?"), steps),
+    }
+
+
+def prefill_flops(D, Ly, F, V, lens_new, lens_old=None):
+    """fp32 FLOPs of a multi-token prefill: the GEMMs of every new row (qkv,
+    out, gate/up, down) plus causal attention (QK^T and PV over the visible
+    keys), plus the lm_head of each sequence's last row."""
+    per_row = 2 * Ly * (3 * D * D + D * D + 2 * D * F + F * D)
+    total = 0
+    for i, n in enumerate(lens_new):
+        old = lens_old[i] if lens_old else 0
+        vis = sum(old + t + 1 for t in range(n))
+        total += n * per_row + Ly * 4 * D * vis + 2 * D * V
+    return total
+
+
+def run_c4(L, args):
+    """8 sequences of 1024 uniform-random tokens prefilled
+    at once (MFMA GEMMs, tiled causal attention writing the KV cache), then 64
+    greedy decode steps of all 8 rows."""
+    V, D, Ly, H, F = 8192, 768, 12, 12, 2048
+    B, T, steps = 8, 1024, args.steps if args.steps != 512 else 64
+    CONFIGS["c4"] = (V, D, Ly, H, F, T, B)
+    ctx, lm, dm = build_model(L, "c4", T + steps + 1)
+    import numpy as np
+    r = L.dnn_rng_seed(SEED["c4"] + 100)
+    ids = np.array([[L.dnn_rng_uniform_int(C.byref(r), V) for _ in range(T)] for _ in range(B)], dtype=np.int32)
+    s = dnn_amd.HipSession(dm, B, T + steps + 1)
+    s.prefill(ids=ids)                              # warm-up pass (buffers, code)
+    s.reset()
+    t0 = time.perf_counter()
+    nxt, _ = s.prefill(ids=ids)
+    pre_wall = time.perf_counter() - t0
+    pre_ms = s.last_ms()
+    t0 = time.perf_counter()
+    out, _ = s.decode(nxt, steps)
+    wall = time.perf_counter() - t0
+    dev_ms = s.last_ms()
+    positions = range(T, T + steps)
+    nbytes = step_bytes(V, D, Ly, F, positions, B)
+    fl = prefill_flops(D, Ly, F, V, [T] * B)
+    return {
+        "tok_s": B * steps / wall, "ms_per_step": wall * 1e3 / steps, "device_ms_per_step": dev_ms / steps,
+        "achieved": nbytes / (dev_ms * 1e-3) / 1e9, "nbytes": nbytes, "kernel": s.kernel(), "B": B, "P": T,
+        "positions": [T, T + steps - 1], "grid": 0,
+        "kernel_desc": ("dnnhip::%s (one persistent launch = %d steps)" if s.kernel() in (3, 4, 5)
+                        else "dnnhip::%s (%d replays)") % (KERNELS.get(s.kernel(), "?"), steps),
+        "prefill": {"tokens": B * T, "ms": round(pre_ms, 3), "wall_ms": round(pre_wall * 1e3, 3),
+                    "tokens_per_s": round(B * T / (pre_ms * 1e-3), 1), "flops": fl,
+                    "tflops": round(fl / (pre_ms * 1e-3) / 1e12, 2), "mfma_fp32_peak_tflops": 157.3,
+                    "frac": round(fl / (pre_ms * 1e-3) / 1e12 / 157.3, 4)},
+    }
+
+
+def run_c5(L, args):
+    """prefix-LM (VLM-shaped) decode, bf16 weights: 64 rows,
+    196 bidirectional patch-embedding rows ~N(0,1) (d=512) then 1..4 causal text
+    tokens (sequence lengths 197..200) prefilled at once, then 16 greedy steps."""
+    import numpy as np
+    V, D, Ly, H, F = 1024, 512, 8, 8, 1024
+    B, I, steps = 64, 196, args.steps if args.steps != 512 else 16
+    CONFIGS["c5"] = (V, D, Ly, H, F, I + 4, B)
+    max_seq = I + 4 + steps + 1
+    ctx = Ctx()
+    n_params = V * D + Ly * (4 * D * D + 3 * D * F + 8 * D + 2 * F) + 2 * V + D
+    assert L.dnn_ctx_init(C.byref(ctx), n_params * 4 + (64 << 20), 16 << 20, 64 << 20) == 0
+    L.dnn_seed(SEED["c5"])
+    lm = L.decoder_lm_create(ctx.params, V, D, Ly, H, D // H, F)
+    L.decoder_lm_init_normal(lm, 0.02)
+    L.decoder_lm_enable_rope(ctx.params, lm, max_seq, 10000.0)
+    L.decoder_lm_device_model_ex.argtypes = [C.c_void_p, C.c_int]
+    L.decoder_lm_device_model_ex.restype = C.c_void_p
+    dm = DeviceModel(L.decoder_lm_device_model_ex(lm, dnn_amd.WEIGHTS_BF16), V, D)
+    r = L.dnn_rng_seed(SEED["c5"] + 100)
+    L.dnn_rng_normal.argtypes = [C.POINTER(Rng)]
+    L.dnn_rng_normal.restype = C.c_float
+    emb = np.array([L.dnn_rng_normal(C.byref(r)) for _ in range(B * I * D)], dtype=np.float32).reshape(B, I, D)
+    n_ids = np.array([1 + L.dnn_rng_uniform_int(C.byref(r), 4) for _ in range(B)], dtype=np.int32)
+    ids = np.array([[L.dnn_rng_uniform_int(C.byref(r), V) for _ in range(4)] for _ in range(B)], dtype=np.int32)
+    s = dnn_amd.HipSession(dm, B, max_seq)
+    s.prefill(ids=ids, n_ids=n_ids, embeds=emb, mode=1, prefix_len=I)     # warm-up pass
+    s.reset()
+    t0 = time.perf_counter()
+    nxt, _ = s.prefill(ids=ids, n_ids=n_ids, embeds=emb, mode=1, prefix_len=I)
+    pre_wall = time.perf_counter() - t0
+    pre_ms = s.last_ms()
+    lens = [int(x) for x in s.lengths()]
+    t0 = time.perf_counter()
+    out, _ = s.decode(nxt, steps)
+    wall = time.perf_counter() - t0
+    dev_ms = s.last_ms()
+    # algorithmic bytes per step: bf16 weight matrices, fp32 biases / gammas,
+    # each row's fp32 K/V history (its own length) read, one K/V row written
+    mats = V * D + Ly * (3 * D * D + D * D + 2 * D * F + F * D)
+    vecs = Ly * (3 * D + D + 2 * D + 2 * F + D) + D + V
+    nbytes = 0
+    for t in range(steps):
+        nbytes += 2 * mats + 4 * vecs + sum(Ly * 2 * (ln + t + 1) * D * 4 + Ly * 2 * D * 4 for ln in lens)
+    fl = prefill_flops(D, Ly, F, V, [I + int(n) for n in n_ids])
+    return {
+        "tok_s": B * steps / wall, "ms_per_step": wall * 1e3 / steps, "device_ms_per_step": dev_ms / steps,
+        "achieved": nbytes / (dev_ms * 1e-3) / 1e9, "nbytes": nbytes, "kernel": s.kernel(), "B": B, "P": I,
+        "positions": [min(lens), max(lens) + steps - 1], "grid": 0, "dtype": "bf16 weights, f32 arithmetic (W16A32)",
+        "kernel_desc": "dnnhip::%s (%d replays)" % (KERNELS.get(s.kernel(), "?"), steps),
+        "prefill": {"tokens": int(sum(lens)), "ms": round(pre_ms, 3), "wall_ms": round(pre_wall * 1e3, 3),
+                    "tokens_per_s": round(sum(lens) / (pre_ms * 1e-3), 1), "flops": fl,
+                    "tflops": round(fl / (pre_ms * 1e-3) / 1e12, 2), "mfma_fp32_peak_tflops": 157.3,
+                    "frac": round(fl / (pre_ms * 1e-3) / 1e12 / 157.3, 4)},
+    }
+
+
+def summary(r):
+    out = {"tokens_per_s": round(r["tok_s"], 2), "ms_per_step": round(r["ms_per_step"], 5),
+           "batch": r["B"], "roofline_achieved_GBps": round(r["achieved"], 1),
+           "roofline_frac": round(r["achieved"] / 8000.0, 4), "kernel": r["kernel_desc"]}
+    if "prefill" in r:
+        out["prefill"] = r["prefill"]
+    return out
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=512)
     ap.add_argument("--warmup", type=int, default=16)
-    ap.add_argument("--config", default="c2", choices=sorted(CONFIGS))
+    ap.add_argument("--config", default="c2", choices=sorted(CONFIGS) + ["c4", "c5"])
     ap.add_argument("--grid", type=int, default=0, help="persistent-kernel workgroups (0 = one per CU)")
     ap.add_argument("--copy-probe", type=int, default=0, metavar="MIB",
                     help="after the timed decode, copy a MIB-sized device buffer 3 times (a plain copy kernel of "
                          "known size, the scale for rocprofv3 FETCH_SIZE / WRITE_SIZE counters)")
     ap.add_argument("--cpu-tokens", type=int, default=24)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-extra", action="store_true", help="the headline workload only (no C3 line)")
     args = ap.parse_args()
     if args.gpus != 1:
         print("bench.py: this build runs on one GPU only (one-GPU boxes); --gpus %d is not supported" % args.gpus,
               file=sys.stderr)
         sys.exit(2)
 
-    V, D, Ly, H, F, P, B = CONFIGS[args.config]
-    max_seq = P + args.warmup + args.steps + 1
     L = host_lib()
     dnn_amd.check(dnn_amd.hip().dnn_hip_init(0))
-    ctx, lm, dm = build_model(L, args.config, max(max_seq, 1088))
-    s = dnn_amd.HipSession(dm, B, max_seq)
-    if args.grid:
-        s.set_grid(args.grid)
-    feed = prompts(L, args.config, V, P, B)
-    ids, _ = s.decode(feed, P)                      # prompt, one token per step
-    if args.warmup:
-        ids, _ = s.decode(ids[-1:], args.warmup)    # warmup (greedy)
-    start_pos = int(s.lengths()[0])
-    t0 = time.perf_counter()
-    ids, _ = s.decode(ids[-1:], args.steps)         # timed: exactly --steps greedy steps
-    wall = time.perf_counter() - t0
-    dev_ms = s.last_ms()
-    assert ids.shape[0] == args.steps
-    positions = range(start_pos, start_pos + args.steps)
-    nbytes = step_bytes(V, D, Ly, F, positions, B)
-    achieved = nbytes / (dev_ms * 1e-3) / 1e9
-    tok_s = B * args.steps / wall
+    cfg = args.config
+    if cfg == "c4":
+        r = run_c4(L, args)
+    elif cfg == "c5":
+        r = run_c5(L, args)
+    else:
+        r = decode_run(L, cfg, args.steps, args.warmup, args.grid)
+    V, D, Ly, H, F, P, B = CONFIGS[cfg]
+    steps = len(range(r["positions"][0], r["positions"][1] + 1)) if cfg not in ("c5",) else (
+        args.steps if args.steps != 512 else 16)
     line = {
         "metric": "decode tokens/sec @1 MI355X (B=1 and B=32) + % of HBM-bandwidth roofline",
-        "value": round(tok_s, 2),
+        "value": round(r["tok_s"], 2),
         "unit": "tokens/s",
         "n_gpus": 1,
-        "steps": args.steps,
+        "steps": steps,
         "warmup": args.warmup,
-        "ms_per_step": round(wall * 1e3 / args.steps, 5),
+        "ms_per_step": round(r["ms_per_step"], 5),
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "f32",
-        "data": "synthetic: seeded N(0,0.02) weights, uniform-random prompt",
-        "config": {"workload": "%s greedy decode, batch %d" % (args.config.upper(), B),
-                   "vocab": V, "d_model": D, "layers": Ly, "heads": H, "ffn": F, "prompt": P,
-                   "batch": B, "positions": [start_pos, start_pos + args.steps - 1], "grid": s.grid()},
-        "device_ms_per_step": round(dev_ms / args.steps, 5),
-        "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": 8000.0, "unit": "GB/s",
-                     "frac": round(achieved / 8000.0, 4), "traffic": None,
-                     "kernel": "dnnhip::%s (one persistent launch = %d steps)" % (KERNELS.get(s.kernel(), "?"), args.steps),
-                     "algorithmic_bytes_per_launch": nbytes},
+        "dtype": "bf16 weights / f32" if cfg == "c5" else "f32",
+        "data": "synthetic: seeded N(0,0.02) weights, uniform-random prompt" + (
+            ", N(0,1) patch embeddings" if cfg == "c5" else ""),
+        "config": {"workload": "%s greedy decode, batch %d" % (cfg.upper(), r["B"]),
+                   "vocab": V, "d_model": D, "layers": Ly, "heads": H, "ffn": F, "prompt": r["P"],
+                   "batch": r["B"], "positions": r["positions"], "grid": r["grid"]},
+        "device_ms_per_step": round(r["device_ms_per_step"], 5),
+        "roofline": {"bound": "hbm", "achieved": round(r["achieved"], 1), "peak": 8000.0, "unit": "GB/s",
+                     "frac": round(r["achieved"] / 8000.0, 4), "traffic": None,
+                     "kernel": r["kernel_desc"], "algorithmic_bytes_per_launch": r["nbytes"]},
     }
-    traffic = measured_traffic(args.config, positions)
+    if "prefill" in r:
+        line["prefill"] = r["prefill"]
+    positions = range(r["positions"][0], r["positions"][1] + 1)
+    traffic = measured_traffic(cfg, positions) if cfg not in ("c4", "c5") else None
     if traffic is not None:
         line["roofline"]["traffic"] = traffic
+    if cfg == "c2" and not args.no_extra:
+        # the metric's second batch size, on the batched engine
+        line["c3_batch32"] = summary(decode_run(L, "c3", 256, 16))
     if args.copy_probe:
         import torch
         x = torch.empty(args.copy_probe << 18, dtype=torch.float32, device="cuda").fill_(1.0)
@@ -220,8 +367,8 @@ def main():
         for _ in range(3):
             y.copy_(x)
         torch.cuda.synchronize()
-    if not args.no_cpu_baseline:
-        line["cpu_baseline"] = cpu_baseline(args.config, args.cpu_tokens)
+    if not args.no_cpu_baseline and cfg in CONFIGS and cfg not in ("c4", "c5"):
+        line["cpu_baseline"] = cpu_baseline(cfg, args.cpu_tokens)
     print(json.dumps(line))
 
 

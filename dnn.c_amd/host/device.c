@@ -17,6 +17,7 @@
 
 typedef struct {
     decoder_lm *lm;
+    int weights;            /* DNN_HIP_WEIGHTS_* */
     dnn_hip_model *dm;
     uint64_t print;
 } mirror;
@@ -74,13 +75,15 @@ static void upload_rope(decoder_lm *lm, dnn_hip_model *dm) {
     else dnn_amd_check(dnn_hip_model_rope(dm, NULL, NULL, 0), "dnn_hip_model_rope");
 }
 
-static mirror *find(decoder_lm *lm) {
+static mirror *find(decoder_lm *lm, int weights) {
     for (int i = 0; i < MAX_MIRRORS; i++)
-        if (g_mirrors[i].lm == lm) return &g_mirrors[i];
+        if (g_mirrors[i].lm == lm && (lm == NULL || g_mirrors[i].weights == weights)) return &g_mirrors[i];
     return NULL;
 }
 
-dnn_hip_model *dnn_amd_device_model(decoder_lm *lm) {
+dnn_hip_model *dnn_amd_device_model(decoder_lm *lm) { return dnn_amd_device_model_ex(lm, DNN_HIP_WEIGHTS_F32); }
+
+dnn_hip_model *dnn_amd_device_model_ex(decoder_lm *lm, int weights) {
     if (!g_device_ready) { dnn_amd_check(dnn_hip_init(0), "dnn_hip_init"); g_device_ready = 1; }
     const int np = 1 + 12 * lm->n_layers + 2;
     const float **ptrs = malloc(sizeof(float *) * (size_t)np);
@@ -88,15 +91,16 @@ dnn_hip_model *dnn_amd_device_model(decoder_lm *lm) {
     int n;
     params_of(lm, ptrs, &n, eps);
     const uint64_t fp = fingerprint(lm);
-    mirror *m = find(lm);
+    mirror *m = find(lm, weights);
     if (!m) {
-        m = find(NULL);
+        m = find(NULL, 0);
         assert(m && "dnn_amd: too many device mirrors; release some with decoder_lm_device_release");
         const transformer_block *b = lm->blocks[0];
-        dnn_amd_check(dnn_hip_model_create(lm->vocab_size, lm->d_model, lm->n_layers, b->n_heads, b->d_k,
-                                           b->ffn->intermediate_size, ptrs, n, eps, &m->dm),
-                      "dnn_hip_model_create");
+        dnn_amd_check(dnn_hip_model_create_ex(lm->vocab_size, lm->d_model, lm->n_layers, b->n_heads, b->d_k,
+                                              b->ffn->intermediate_size, ptrs, n, eps, weights, &m->dm),
+                      "dnn_hip_model_create_ex");
         m->lm = lm;
+        m->weights = weights;
         upload_rope(lm, m->dm);
         m->print = fp;
     } else if (m->print != fp) {
@@ -110,17 +114,28 @@ dnn_hip_model *dnn_amd_device_model(decoder_lm *lm) {
 }
 
 void decoder_lm_device_sync(decoder_lm *lm) {
-    mirror *m = find(lm);
-    if (m) m->print = 0;
+    for (int w = DNN_HIP_WEIGHTS_F32; w <= DNN_HIP_WEIGHTS_BF16; w++) {
+        mirror *m = find(lm, w);
+        if (m) {
+            m->print = 0;
+            (void)dnn_amd_device_model_ex(lm, w);
+        }
+    }
     (void)dnn_amd_device_model(lm);
 }
 
 void decoder_lm_device_release(decoder_lm *lm) {
-    mirror *m = find(lm);
-    if (!m) return;
-    dnn_hip_model_destroy(m->dm);
-    m->lm = NULL;
-    m->dm = NULL;
+    for (int w = DNN_HIP_WEIGHTS_F32; w <= DNN_HIP_WEIGHTS_BF16; w++) {
+        mirror *m = find(lm, w);
+        if (!m) continue;
+        dnn_hip_model_destroy(m->dm);
+        m->lm = NULL;
+        m->dm = NULL;
+    }
 }
 
 struct dnn_hip_model *decoder_lm_device_model(decoder_lm *lm) { return dnn_amd_device_model(lm); }
+
+struct dnn_hip_model *decoder_lm_device_model_ex(decoder_lm *lm, int weights) {
+    return dnn_amd_device_model_ex(lm, weights);
+}

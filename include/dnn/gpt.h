@@ -45,6 +45,9 @@ void decoder_lm_device_release(decoder_lm *lm);
 /* The mirror itself, for callers that drive sessions through include/dnn_hip.h
  * (batched decode, timing).  Owned by the library. */
 struct dnn_hip_model *decoder_lm_device_model(decoder_lm *lm);
+/* A mirror with a choice of weight storage: 0 = fp32 (the one generate uses),
+ * 1 = bf16-rounded weight matrices (DNN_HIP_WEIGHTS_BF16 of dnn_hip.h). */
+struct dnn_hip_model *decoder_lm_device_model_ex(decoder_lm *lm, int weights);
 
 /* Synthetic initialisation used by the parity and bench configurations (no
  * counterpart in the reference): every parameter except the RMSNorm gammas is
