@@ -181,6 +181,24 @@ def decode_run(L, cfg, steps, warmup, grid=0):
     }
 
 
+def copy_probe(nbytes):
+    """Three device-to-device copies of nbytes (the runtime's blit kernel): a
+    plain copy of known size, the scale for the FETCH_SIZE / WRITE_SIZE counters."""
+    rt = C.CDLL("libamdhip64.so")
+    rt.hipMalloc.argtypes = [C.POINTER(C.c_void_p), C.c_size_t]
+    rt.hipMemset.argtypes = [C.c_void_p, C.c_int, C.c_size_t]
+    rt.hipMemcpy.argtypes = [C.c_void_p, C.c_void_p, C.c_size_t, C.c_int]
+    rt.hipFree.argtypes = [C.c_void_p]
+    a, b = C.c_void_p(), C.c_void_p()
+    assert rt.hipMalloc(C.byref(a), nbytes) == 0 and rt.hipMalloc(C.byref(b), nbytes) == 0
+    assert rt.hipMemset(a, 1, nbytes) == 0
+    for _ in range(3):
+        assert rt.hipMemcpy(b, a, nbytes, 3) == 0          # hipMemcpyDeviceToDevice
+    assert rt.hipDeviceSynchronize() == 0
+    rt.hipFree(a)
+    rt.hipFree(b)
+
+
 def prefill_flops(D, Ly, F, V, lens_new, lens_old=None):
     """fp32 FLOPs of a multi-token prefill: the GEMMs of every new row (qkv,
     out, gate/up, down) plus causal attention (QK^T and PV over the visible
@@ -361,12 +379,7 @@ def main():
         # the metric's second batch size, on the batched engine
         line["c3_batch32"] = summary(decode_run(L, "c3", 256, 16))
     if args.copy_probe:
-        import torch
-        x = torch.empty(args.copy_probe << 18, dtype=torch.float32, device="cuda").fill_(1.0)
-        y = torch.empty_like(x)
-        for _ in range(3):
-            y.copy_(x)
-        torch.cuda.synchronize()
+        copy_probe(args.copy_probe << 20)
     if not args.no_cpu_baseline and cfg in CONFIGS and cfg not in ("c4", "c5"):
         line["cpu_baseline"] = cpu_baseline(cfg, args.cpu_tokens)
     print(json.dumps(line))
