@@ -255,17 +255,18 @@ int enqueue_layer(dnn_hip_session *s, int l, const PrefillPlan *pp) {
 }
 
 // final rms_norm -> tied lm_head -> argmax (+ the next step's feed in decode)
-int enqueue_head(dnn_hip_session *s, const PrefillPlan *pp, float *logits, int *ids, int eos) {
+int enqueue_head(dnn_hip_session *s, const PrefillPlan *pp, float *logits, int *ids, int eos, int rows = 0,
+                 bool norm = true) {
     dnn_hip_model *m = s->m;
     BatchEngine *e = s->eng;
     const Wts W{m};
     const uint32_t embed = (uint32_t)(m->off.embed / 4), lm_bias = (uint32_t)(m->off.lm_bias / 4),
                    g_final = (uint32_t)(m->off.g_final / 4);
     GemmArgs g = gemm_base(s, W, embed, m->ldD, m->V, m->ldD);
-    g.A = e->X; g.lda = m->ldD; g.M = s->B;
+    g.A = e->X; g.lda = m->ldD; g.M = rows > 0 ? rows : s->B;
     g.arow = pp ? pp->arow : nullptr;
     g.bias = W.f(lm_bias);
-    g.gamma = W.f(g_final); g.eps = m->eps_final; g.dnorm = m->D;
+    g.gamma = norm ? W.f(g_final) : nullptr; g.eps = m->eps_final; g.dnorm = m->D;
     g.amax = e->amax; g.head_cnt = e->cnt + CNT_GEMM + CNT_ATT;
     g.logits = logits; g.ids = ids;
     g.feed = s->feed; g.n_feed = s->n_feed; g.pos = s->pos;
@@ -273,10 +274,10 @@ int enqueue_head(dnn_hip_session *s, const PrefillPlan *pp, float *logits, int *
     g.steps_done = e->steps_done; g.eos = eos; g.row_done = e->row_done;
     g.prefill = pp != nullptr;
     g.kslot = 5 * m->L;
-    g.ks = pick_ks((m->V + 15) / 16, m->ldD, s->B, true);
+    g.ks = pick_ks((m->V + 15) / 16, m->ldD, g.M, true);
     g.amax_tiles = (m->V + 15) / 16;
     g.part = e->part; g.cnt = e->cnt;
-    HIP_TRY(launch_gemm(EPI_HEAD, true, m->bf16 != 0, false, g, s->stream));
+    HIP_TRY(launch_gemm(EPI_HEAD, norm, m->bf16 != 0, false, g, s->stream));
     HIP_TRY(launch_head_finish(g, s->stream));
     return DNN_HIP_OK;
 }
@@ -436,6 +437,127 @@ int engine_prefill(dnn_hip_session *s, const float *embeds, int n_embed, const i
     if (logits) HIP_TRY(hipMemcpy(logits, e->pre_logits, sizeof(float) * (size_t)B * m->V, hipMemcpyDeviceToHost));
     for (int b = 0; b < B; b++) s->h_pos[b] = p0[b] + nn[b];
     HIP_TRY(hipMemcpy(s->pos, s->h_pos.data(), sizeof(int) * B, hipMemcpyHostToDevice));
+    return DNN_HIP_OK;
+}
+
+
+// One block over n_new rows of every batch row at positions pos0.. (the
+// reference's per-layer cached forward: the caller's cache length is pos0).
+int engine_block(dnn_hip_session *s, int layer, const float *x, int n_new, int pos0, int mode, int prefix_len,
+                 float *y) {
+    dnn_hip_model *m = s->m;
+    const int B = s->B, D = m->D, M = B * n_new;
+    if (layer < 0 || layer >= m->L) return set_error(DNN_HIP_EINVAL, "layer %d of %d", layer, m->L);
+    if (!x || !y || n_new < 1 || pos0 < 0) return set_error(DNN_HIP_EINVAL, "bad block input (n_new %d, pos0 %d)", n_new, pos0);
+    if (mode != 0 && mode != 1) return set_error(DNN_HIP_EINVAL, "mode %d: 0 (causal) or 1 (prefix-LM)", mode);
+    if (mode == 1 && pos0 != 0) return set_error(DNN_HIP_EINVAL, "prefix-LM needs an empty cache (position %d)", pos0);
+    if (pos0 + n_new > s->max_seq)
+        return set_error(DNN_HIP_ERANGE, "%d cached + %d new exceeds max_seq %d", pos0, n_new, s->max_seq);
+    if (m->rope && pos0 + n_new > m->rope_rows)
+        return set_error(DNN_HIP_ERANGE, "position %d beyond the RoPE table (%d rows)", pos0 + n_new - 1, m->rope_rows);
+    HIP_TRY(hipSetDevice(m->device));
+    int rc = engine_get(s, M);
+    if (rc) return rc;
+    BatchEngine *e = s->eng;
+    std::vector<int> tiles;
+    for (int b = 0; b < B; b++)
+        for (int t0 = 0; t0 < n_new; t0 += 64) { tiles.push_back(b); tiles.push_back(t0); }
+    const int T = (int)tiles.size() / 2;
+    std::vector<int> plan((size_t)3 * M + 4 * B + tiles.size());
+    int *row_b = plan.data(), *row_p = row_b + M, *pid = row_p + M, *hrow0 = pid + M, *hnn = hrow0 + B,
+        *hp0 = hnn + B, *harow = hp0 + B, *htiles = harow + B;
+    for (int b = 0; b < B; b++) {
+        for (int t = 0; t < n_new; t++) {
+            row_b[b * n_new + t] = b;
+            row_p[b * n_new + t] = pos0 + t;
+            pid[b * n_new + t] = -1;
+        }
+        hrow0[b] = b * n_new; hnn[b] = n_new; hp0[b] = pos0; harow[b] = b * n_new + n_new - 1;
+    }
+    std::copy(tiles.begin(), tiles.end(), htiles);
+    rc = grow(&e->pre_i, &e->pre_cap, plan.size());
+    if (rc) return rc;
+    HIP_TRY(hipMemcpyAsync(e->pre_i, plan.data(), plan.size() * sizeof(int), hipMemcpyHostToDevice, s->stream));
+    int *d = e->pre_i;
+    PrefillPlan pp{M, d, d + M, d + 2 * M, d + 3 * M, d + 3 * M + B, d + 3 * M + 2 * B, d + 3 * M + 3 * B,
+                   d + 3 * M + 4 * B, T, mode, prefix_len};
+    HIP_TRY(hipMemcpy2DAsync(e->X, (size_t)m->ldD * 4, x, (size_t)D * 4, (size_t)D * 4, M, hipMemcpyHostToDevice, s->stream));
+    HIP_TRY(hipEventRecord(s->ev0, s->stream));
+    rc = enqueue_layer(s, layer, &pp);
+    if (rc) return rc;
+    HIP_TRY(hipEventRecord(s->ev1, s->stream));
+    HIP_TRY(hipMemcpy2DAsync(y, (size_t)D * 4, e->X, (size_t)m->ldD * 4, (size_t)D * 4, M, hipMemcpyDeviceToHost, s->stream));
+    HIP_TRY(hipStreamSynchronize(s->stream));
+    HIP_TRY(hipEventElapsedTime(&s->last_ms, s->ev0, s->ev1));
+    return DNN_HIP_OK;
+}
+
+// logits [n][V] of n rows (optionally through the final rms_norm first), in
+// chunks of up to 64 rows of the decode-shape lm_head GEMM.
+int engine_head(dnn_hip_session *s, const float *x, int n, int norm, float *logits) {
+    dnn_hip_model *m = s->m;
+    const int D = m->D;
+    if (!x || !logits || n < 1) return set_error(DNN_HIP_EINVAL, "bad head input (%d rows)", n);
+    HIP_TRY(hipSetDevice(m->device));
+    int rc = engine_get(s, n);
+    if (rc) return rc;
+    BatchEngine *e = s->eng;
+    std::vector<int> rows(n);
+    for (int i = 0; i < n; i++) rows[i] = i;
+    rc = grow(&e->pre_i, &e->pre_cap, (size_t)n);
+    if (rc) return rc;
+    HIP_TRY(hipMemcpyAsync(e->pre_i, rows.data(), (size_t)n * sizeof(int), hipMemcpyHostToDevice, s->stream));
+    HIP_TRY(hipMemcpy2DAsync(e->X, (size_t)m->ldD * 4, x, (size_t)D * 4, (size_t)D * 4, n, hipMemcpyHostToDevice, s->stream));
+    for (int r0 = 0; r0 < n; r0 += BK_MAXM) {
+        const int cnt = std::min(BK_MAXM, n - r0);
+        PrefillPlan pp{};
+        pp.arow = e->pre_i + r0;
+        rc = enqueue_head(s, &pp, e->pre_logits, e->next_ids, -1, cnt, norm != 0);
+        if (rc) return rc;
+        HIP_TRY(hipMemcpyAsync(logits + (size_t)r0 * m->V, e->pre_logits, sizeof(float) * (size_t)cnt * m->V,
+                               hipMemcpyDeviceToHost, s->stream));
+    }
+    HIP_TRY(hipStreamSynchronize(s->stream));
+    return DNN_HIP_OK;
+}
+
+// Embedding rows of n token ids (embedding.c:79-84) into out [n][d_model].
+int engine_embed(dnn_hip_session *s, const int *ids, int n, float *out) {
+    dnn_hip_model *m = s->m;
+    if (!ids || !out || n < 1) return set_error(DNN_HIP_EINVAL, "bad embedding input (%d ids)", n);
+    for (int i = 0; i < n; i++)
+        if (ids[i] < 0 || ids[i] >= m->V) return set_error(DNN_HIP_ERANGE, "token id %d outside [0,%d)", ids[i], m->V);
+    HIP_TRY(hipSetDevice(m->device));
+    int rc = engine_get(s, n);
+    if (rc) return rc;
+    BatchEngine *e = s->eng;
+    rc = grow(&e->pre_i, &e->pre_cap, (size_t)n);
+    if (rc) return rc;
+    HIP_TRY(hipMemcpyAsync(e->pre_i, ids, (size_t)n * sizeof(int), hipMemcpyHostToDevice, s->stream));
+    EmbedArgs ea{};
+    ea.embed = reinterpret_cast<const float *>(m->arena) + m->off.embed / 4;
+    ea.ids = e->pre_i; ea.out = e->X; ea.M = n; ea.ld = m->ldD; ea.D = m->D;
+    HIP_TRY(launch_embed(ea, s->stream));
+    HIP_TRY(hipMemcpy2DAsync(out, (size_t)m->D * 4, e->X, (size_t)m->ldD * 4, (size_t)m->D * 4, n, hipMemcpyDeviceToHost, s->stream));
+    HIP_TRY(hipStreamSynchronize(s->stream));
+    return DNN_HIP_OK;
+}
+
+// rms_norm of n rows of d values with a caller's gamma (rms_norm_forward,
+// nn.c:169-173): x, gamma, y in host memory.
+int engine_rms_norm(dnn_hip_session *s, const float *x, const float *gamma, int n, int d, float eps, float *y) {
+    dnn_hip_model *m = s->m;
+    if (!x || !gamma || !y || n < 1 || d < 1 || d > m->ldD) return set_error(DNN_HIP_EINVAL, "bad rms_norm input (%d x %d)", n, d);
+    HIP_TRY(hipSetDevice(m->device));
+    int rc = engine_get(s, n);
+    if (rc) return rc;
+    BatchEngine *e = s->eng;
+    float *g = e->X1;                                  // gamma in row 0 of X1, rows of x in X, y into ATT
+    HIP_TRY(hipMemcpyAsync(g, gamma, sizeof(float) * d, hipMemcpyHostToDevice, s->stream));
+    HIP_TRY(hipMemcpy2DAsync(e->X, (size_t)m->ldD * 4, x, (size_t)d * 4, (size_t)d * 4, n, hipMemcpyHostToDevice, s->stream));
+    HIP_TRY(launch_rms_rows(e->X, g, e->ATT, n, d, m->ldD, eps, s->stream));
+    HIP_TRY(hipMemcpy2DAsync(y, (size_t)d * 4, e->ATT, (size_t)m->ldD * 4, (size_t)d * 4, n, hipMemcpyDeviceToHost, s->stream));
+    HIP_TRY(hipStreamSynchronize(s->stream));
     return DNN_HIP_OK;
 }
 

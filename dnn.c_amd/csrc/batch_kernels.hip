@@ -858,6 +858,25 @@ __global__ __launch_bounds__(NTHR) void embed_kernel(const EmbedArgs a) {
 }
 
 // ---------------------------------------------------------------------------
+// rms_norm of rows (norm.c:433-440, 466-471): y = (x * rs) * gamma with
+// rs = 1 / sqrtf(sum(x^2) * (1/d) + eps); one workgroup per row.
+__global__ __launch_bounds__(NTHR) void rms_rows_kernel(const float *x, const float *gamma, float *y, int d, int ld,
+                                                        float eps) {
+    __shared__ float s_part[NTHR / 64];
+    const int r = blockIdx.x, tid = threadIdx.x;
+    const float *xr = x + (size_t)r * ld;
+    float ss = 0.f;
+    for (int c = tid; c < d; c += NTHR) ss += xr[c] * xr[c];
+    ss = wave_sum(ss);
+    if ((tid & 63) == 0) s_part[tid >> 6] = ss;
+    __syncthreads();
+    float tot = 0.f;
+    for (int w = 0; w < NTHR / 64; w++) tot += s_part[w];
+    const float rs = 1.0f / sqrtf(tot * (1.0f / (float)d) + eps);
+    for (int c = tid; c < d; c += NTHR) y[(size_t)r * ld + c] = (xr[c] * rs) * gamma[c];
+}
+
+// ---------------------------------------------------------------------------
 // launchers
 
 namespace {
@@ -920,7 +939,7 @@ hipError_t gemm_any(int epi, bool norm, bool prefill, const GemmArgs &g, hipStre
         case EPI_QKV: return norm ? gemm_decode<EPI_QKV, true, BF>(g, st) : hipErrorInvalidValue;
         case EPI_RES: return norm ? hipErrorInvalidValue : gemm_decode<EPI_RES, false, BF>(g, st);
         case EPI_SWIGLU: return norm ? gemm_decode<EPI_SWIGLU, true, BF>(g, st) : hipErrorInvalidValue;
-        case EPI_HEAD: return norm ? gemm_decode<EPI_HEAD, true, BF>(g, st) : hipErrorInvalidValue;
+        case EPI_HEAD: return norm ? gemm_decode<EPI_HEAD, true, BF>(g, st) : gemm_decode<EPI_HEAD, false, BF>(g, st);
         default: return hipErrorInvalidValue;
     }
 }
@@ -944,6 +963,12 @@ hipError_t launch_attn(const AttnArgs &a, hipStream_t stream) {
 
 hipError_t launch_prefill_attn(const PrefillAttnArgs &a, hipStream_t stream) {
     hipLaunchKernelGGL(prefill_attn_kernel, dim3(a.n_tiles, a.H), dim3(NTHR), 0, stream, a);
+    return hipGetLastError();
+}
+
+hipError_t launch_rms_rows(const float *x, const float *gamma, float *y, int n, int d, int ld, float eps,
+                           hipStream_t stream) {
+    hipLaunchKernelGGL(rms_rows_kernel, dim3(n), dim3(NTHR), 0, stream, x, gamma, y, d, ld, eps);
     return hipGetLastError();
 }
 

@@ -579,6 +579,49 @@ int dnn_hip_prefill(dnn_hip_session *s, const float *embeds, int n_embed, const 
     return engine_prefill(s, embeds, n_embed, ids, n_ids_max, n_ids, mode, prefix_len, next_ids, logits);
 }
 
+int dnn_hip_block_forward(dnn_hip_session *s, int layer, const float *x, int n_new, int pos0, int mode,
+                          int prefix_len, float *y) {
+    if (!s) return fail(DNN_HIP_EINVAL, "session is NULL");
+    return engine_block(s, layer, x, n_new, pos0, mode, prefix_len, y);
+}
+
+int dnn_hip_head_forward(dnn_hip_session *s, const float *x, int n, int norm, float *logits) {
+    if (!s) return fail(DNN_HIP_EINVAL, "session is NULL");
+    return engine_head(s, x, n, norm, logits);
+}
+
+int dnn_hip_embed(dnn_hip_session *s, const int *ids, int n, float *out) {
+    if (!s) return fail(DNN_HIP_EINVAL, "session is NULL");
+    return engine_embed(s, ids, n, out);
+}
+
+int dnn_hip_rms_norm(dnn_hip_session *s, const float *x, const float *gamma, int n, int d, float eps, float *y) {
+    if (!s) return fail(DNN_HIP_EINVAL, "session is NULL");
+    return engine_rms_norm(s, x, gamma, n, d, eps, y);
+}
+
+int dnn_hip_cache_read(dnn_hip_session *s, int layer, int which, int len, float *out) {
+    if (!s || !out) return fail(DNN_HIP_EINVAL, "NULL argument");
+    dnn_hip_model *m = s->m;
+    if (layer < 0 || layer >= m->L || (which != 0 && which != 1) || len < 0 || len > s->max_seq)
+        return fail(DNN_HIP_EINVAL, "layer %d / which %d / len %d", layer, which, len);
+    HIP_TRY(hipSetDevice(m->device));
+    const size_t per = (size_t)m->H * DK * s->kv_s;           // floats per (layer, row)
+    std::vector<float> h((size_t)s->B * per);
+    const float *src = (which == 0 ? s->kc : s->vc) + (size_t)layer * s->B * per;
+    HIP_TRY(hipStreamSynchronize(s->stream));
+    HIP_TRY(hipMemcpy(h.data(), src, h.size() * sizeof(float), hipMemcpyDeviceToHost));
+    for (int b = 0; b < s->B; b++)
+        for (int hh = 0; hh < m->H; hh++) {
+            const float *hd = h.data() + ((size_t)b * m->H + hh) * DK * s->kv_s;
+            float *o = out + (((size_t)b * m->H + hh) * len) * DK;
+            for (int p = 0; p < len; p++)
+                for (int d = 0; d < DK; d++)
+                    o[(size_t)p * DK + d] = which == 0 ? hd[(size_t)d * s->kv_s + p] : hd[(size_t)p * DK + d];
+        }
+    return DNN_HIP_OK;
+}
+
 int dnn_hip_generate(dnn_hip_model *m, const int *prompt, int P, int max_new, int eos, int *out, int *n_out) {
     if (!m || !prompt || !out || !n_out) return fail(DNN_HIP_EINVAL, "NULL argument");
     if (P <= 0 || max_new <= 0) return fail(DNN_HIP_EINVAL, "prompt %d / max_new %d", P, max_new);

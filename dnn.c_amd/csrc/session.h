@@ -114,6 +114,11 @@ int engine_decode(dnn_hip_session *s, const int *feed, int n_feed_all, const int
                   int *ids, float *logits, int *steps_done);
 int engine_prefill(dnn_hip_session *s, const float *embeds, int n_embed, const int *ids, int n_ids_max,
                    const int *n_ids, int mode, int prefix_len, int *next_ids, float *logits);
+int engine_block(dnn_hip_session *s, int layer, const float *x, int n_new, int pos0, int mode, int prefix_len,
+                 float *y);
+int engine_head(dnn_hip_session *s, const float *x, int n, int norm, float *logits);
+int engine_embed(dnn_hip_session *s, const int *ids, int n, float *out);
+int engine_rms_norm(dnn_hip_session *s, const float *x, const float *gamma, int n, int d, float eps, float *y);
 void engine_destroy(BatchEngine *e);
 
 }  // namespace dnnhip

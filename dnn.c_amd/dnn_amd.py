@@ -24,6 +24,7 @@ HIP_SYMBOLS = [
     "dnn_hip_session_reset", "dnn_hip_session_lengths", "dnn_hip_session_destroy",
     "dnn_hip_decode", "dnn_hip_generate", "dnn_hip_session_last_ms", "dnn_hip_session_set_grid",
     "dnn_hip_session_grid", "dnn_hip_session_kernel", "dnn_hip_model_create_ex", "dnn_hip_prefill",
+    "dnn_hip_block_forward", "dnn_hip_head_forward", "dnn_hip_embed", "dnn_hip_cache_read", "dnn_hip_rms_norm",
 ]
 
 WEIGHTS_F32 = 0
@@ -63,6 +64,11 @@ def hip():
         L.dnn_hip_model_create_ex.argtypes = [C.c_int] * 6 + [C.POINTER(f32p), C.c_int, f32p, C.c_int,
                                                               C.POINTER(C.c_void_p)]
         L.dnn_hip_prefill.argtypes = [C.c_void_p, f32p, C.c_int, i32p, C.c_int, i32p, C.c_int, C.c_int, i32p, f32p]
+        L.dnn_hip_block_forward.argtypes = [C.c_void_p, C.c_int, f32p, C.c_int, C.c_int, C.c_int, C.c_int, f32p]
+        L.dnn_hip_head_forward.argtypes = [C.c_void_p, f32p, C.c_int, C.c_int, f32p]
+        L.dnn_hip_embed.argtypes = [C.c_void_p, i32p, C.c_int, f32p]
+        L.dnn_hip_cache_read.argtypes = [C.c_void_p, C.c_int, C.c_int, C.c_int, f32p]
+        L.dnn_hip_rms_norm.argtypes = [C.c_void_p, f32p, f32p, C.c_int, C.c_int, C.c_float, f32p]
         _hip = L
     return _hip
 
@@ -171,6 +177,39 @@ class HipSession:
                                     _ip(nid) if nid is not None else None, mode, prefix_len, _ip(nxt),
                                     _fp(lg) if want_logits else None))
         return nxt, lg
+
+    def block_forward(self, layer, x, pos0, mode=0, prefix_len=0):
+        """x [B][n_new][D] -> y [B][n_new][D] through one block at positions pos0.."""
+        x = np.ascontiguousarray(x, dtype=np.float32)
+        y = np.zeros_like(x)
+        check(hip().dnn_hip_block_forward(self.ptr, layer, _fp(x), x.shape[1], pos0, mode, prefix_len, _fp(y)))
+        return y
+
+    def head_forward(self, x, norm=True):
+        x = np.ascontiguousarray(x, dtype=np.float32).reshape(-1, self.m.D)
+        lg = np.zeros((x.shape[0], self.m.V), dtype=np.float32)
+        check(hip().dnn_hip_head_forward(self.ptr, _fp(x), x.shape[0], 1 if norm else 0, _fp(lg)))
+        return lg
+
+    def embed(self, ids):
+        ids = np.ascontiguousarray(ids, dtype=np.int32).reshape(-1)
+        out = np.zeros((len(ids), self.m.D), dtype=np.float32)
+        check(hip().dnn_hip_embed(self.ptr, _ip(ids), len(ids), _fp(out)))
+        return out
+
+    def rms_norm(self, x, gamma, eps=1e-5):
+        """rms_norm of the rows of x [n][d] with gamma [d], on the device."""
+        x = np.ascontiguousarray(x, dtype=np.float32)
+        g = np.ascontiguousarray(gamma, dtype=np.float32)
+        y = np.zeros_like(x)
+        d = x.shape[-1]
+        check(hip().dnn_hip_rms_norm(self.ptr, _fp(x), _fp(g), x.size // d, d, C.c_float(eps), _fp(y)))
+        return y
+
+    def cache_read(self, layer, which, length):
+        out = np.zeros((self.B, self.m.H, length, 64), dtype=np.float32)
+        check(hip().dnn_hip_cache_read(self.ptr, layer, which, length, _fp(out)))
+        return out
 
     def last_ms(self):
         ms = C.c_float()

@@ -53,6 +53,7 @@ decoder_lm *decoder_lm_create(struct mem_pool *params_pool, int vocab_size, int 
     lm->lm_head->bias = tensor_zeros(params_pool, 1, (int[]){vocab_size}, 1);
     module_param(&lm->lm_head->base, "bias", lm->lm_head->bias);
     module_add_child(&lm->base, "lm_head", &lm->lm_head->base);
+    dnn_amd_register_lm(lm);
     return lm;
 }
 

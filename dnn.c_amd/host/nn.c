@@ -4,6 +4,7 @@
 #include "dnn/nn.h"
 #include <assert.h>
 #include <math.h>
+#include <string.h>
 
 linear *linear_create(struct mem_pool *params, int in_features, int out_features) {
     assert(in_features > 0 && out_features > 0);
@@ -61,3 +62,22 @@ embedding *embedding_create(struct mem_pool *params, int vocab_size, int d_model
 long long linear_num_parameters(linear *l) { return module_num_parameters(&l->base); }
 long long swiglu_ffn_num_parameters(swiglu_ffn *f) { return module_num_parameters(&f->base); }
 long long embedding_num_parameters(embedding *e) { return module_num_parameters(&e->base); }
+
+/* Row gather from the host table (embedding.c:79-84); the decode kernels do
+ * their own gather from the HBM mirror. */
+tensor *embedding_forward(struct mem_pool *scratch, struct mem_pool *data, embedding *emb, const tensor *ids) {
+    (void)data;
+    assert(emb && ids && ids->ndim == 1 && "embedding: ids must be 1D");
+    const tensor *w = emb->weight;
+    assert(w->ndim == 2 && w->contiguous && "embedding: table must be 2D, contiguous");
+    const int V = w->shape[0], D = w->shape[1], N = ids->shape[0];
+    tensor *out = tensor_scratch(scratch, 2, (int[]){N, D}, 0);
+    const int *id = (const int *)ids->data + ids->offset;
+    const float *td = (const float *)w->data + w->offset;
+    for (int i = 0; i < N; i++) {
+        const int v = id[(size_t)i * ids->strides[0]];
+        assert(v >= 0 && v < V && "embedding: id out of range");
+        memcpy((float *)out->data + (size_t)i * D, td + (size_t)v * D, sizeof(float) * (size_t)D);
+    }
+    return out;
+}

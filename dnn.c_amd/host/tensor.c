@@ -110,6 +110,43 @@ tensor *tensor_flatten(struct mem_pool *scratch, tensor *t) {
     return tensor_reshape(scratch, t, 1, (int[]){-1});
 }
 
+/* Copies every element of src (any strides) into the packed out tensor at
+ * offset `at` along dim. */
+static void cat_part(float *out, const int *oshape, int ndim, int dim, int at, const tensor *src) {
+    int idx[DNN_MAX_DIMS] = {0};
+    const int n = count(src->shape, ndim);
+    const float *sd = (const float *)src->data;
+    for (int i = 0; i < n; i++) {
+        size_t so = (size_t)src->offset, oo = 0;
+        for (int d = 0; d < ndim; d++) {
+            so += (size_t)idx[d] * src->strides[d];
+            oo = oo * oshape[d] + (size_t)(idx[d] + (d == dim ? at : 0));
+        }
+        out[oo] = sd[so];
+        for (int d = ndim - 1; d >= 0; d--) {
+            if (++idx[d] < src->shape[d]) break;
+            idx[d] = 0;
+        }
+    }
+}
+
+tensor *tensor_cat(struct mem_pool *scratch, const tensor *a, const tensor *b, int dim) {
+    assert(a && b && a->ndim == b->ndim && "tensor_cat: ndim must match");
+    const int ndim = a->ndim;
+    if (dim < 0) dim += ndim;
+    assert(dim >= 0 && dim < ndim && "tensor_cat: dim out of range");
+    int shape[DNN_MAX_DIMS];
+    for (int d = 0; d < ndim; d++) {
+        assert((d == dim || a->shape[d] == b->shape[d]) && "tensor_cat: shape mismatch");
+        shape[d] = a->shape[d];
+    }
+    shape[dim] += b->shape[dim];
+    tensor *out = tensor_scratch(scratch, ndim, shape, 0);
+    cat_part((float *)out->data, shape, ndim, dim, 0, a);
+    cat_part((float *)out->data, shape, ndim, dim, a->shape[dim], b);
+    return out;
+}
+
 float *tensor_data_ptr(tensor *t) {
     assert(tensor_is_contiguous(t));
     return (float *)t->data + t->offset;

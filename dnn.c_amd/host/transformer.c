@@ -1,7 +1,9 @@
 /* transformer.c -- KV cache and block construction (reference
- * src/transformer.c:30-147).  The cached forward itself runs on the device,
- * inside the decode kernel (dnn.c_amd/csrc/decode_kernel.hip). */
+ * src/transformer.c:30-147).  The cached forward runs on the device (blocks.c
+ * for the per-block API, the decode kernels for generate); a cache it used
+ * holds its rows in HBM, and kv_cache_get_K/V copy them back first. */
 #include "dnn/transformer.h"
+#include "device.h"
 #include <assert.h>
 #include <string.h>
 
@@ -22,6 +24,7 @@ void kv_cache_append(kv_cache *c, const tensor *K_new, const tensor *V_new) {
     assert(B == c->k_cache->shape[0] && H == c->k_cache->shape[1] && D == c->k_cache->shape[3]);
     assert(N == V_new->shape[2]);
     assert(c->seq_len + N <= c->max_seq && "kv_cache_append: cache full");
+    assert(!dnn_amd_cache_is_bound(c) && "kv_cache_append: the cache's rows live on the device (block forward)");
     const size_t row = (size_t)N * D * sizeof(float);
     for (int b = 0; b < B; b++)
         for (int h = 0; h < H; h++) {
@@ -36,11 +39,13 @@ void kv_cache_append(kv_cache *c, const tensor *K_new, const tensor *V_new) {
 
 tensor *kv_cache_get_K(struct mem_pool *scratch, kv_cache *c) {
     assert(c && c->seq_len > 0 && "kv_cache_get_K: empty cache");
+    dnn_amd_cache_sync(c);
     return tensor_slice(scratch, c->k_cache, 2, 0, c->seq_len);
 }
 
 tensor *kv_cache_get_V(struct mem_pool *scratch, kv_cache *c) {
     assert(c && c->seq_len > 0 && "kv_cache_get_V: empty cache");
+    dnn_amd_cache_sync(c);
     return tensor_slice(scratch, c->v_cache, 2, 0, c->seq_len);
 }
 

@@ -27,6 +27,23 @@ void        decoder_lm_enable_rope(struct mem_pool *params_pool, decoder_lm *lm,
 long long   decoder_lm_num_parameters(decoder_lm *lm);
 
 int decoder_lm_argmax_token(const float *logits, int vocab_size);
+
+/* h [..., d_model] -> logits [..., V] = h . embed^T + lm_head bias (the tied
+ * head, gpt.c:117-122; no final norm).  On the device. */
+tensor *decoder_lm_lm_head_forward(struct mem_pool *scratch, decoder_lm *lm, const tensor *h);
+/* input_ids [B, N] int32 -> embeddings [B, N, d_model] (gpt.c:66-81). */
+tensor *decoder_lm_token_embeds(struct mem_pool *scratch, decoder_lm *lm, const tensor *input_ids);
+/* embeds [B, S, d_model] -> logits [B, S, V]: every block (full-sequence
+ * attention with the mode's mask), final rms_norm, tied lm_head
+ * (gpt.c:84-144).  seq_lens (or NULL) gives each batch row's valid length: its
+ * rows at or past that length are not computed by the reference
+ * (attention.c:272-285); here they come back as zero logits.  On the device. */
+tensor *decoder_lm_forward_embeds_ex(struct mem_pool *scratch, decoder_lm *lm, const tensor *embeds,
+                                     attention_mode mode, int prefix_len, const int *seq_lens);
+tensor *decoder_lm_forward_embeds(struct mem_pool *scratch, decoder_lm *lm, const tensor *embeds);
+/* input_ids [B, N] int32 -> logits [B, N, V]: full causal forward (gpt.c:148-151).
+ * On the device. */
+tensor *decoder_lm_forward(struct mem_pool *scratch, decoder_lm *lm, const tensor *input_ids);
 int decoder_lm_sample_with_temp(const float *logits, int vocab_size, float temp);
 
 /* Greedy (temperature 0) or sampled generation.  prompt_ids [1, N] int32.

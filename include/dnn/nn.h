@@ -41,6 +41,15 @@ swiglu_ffn *swiglu_ffn_create(struct mem_pool *params, int d_model, int intermed
 rms_norm   *rms_norm_create(struct mem_pool *params, int d, float eps);
 embedding  *embedding_create(struct mem_pool *params, int vocab_size, int d_model);
 
+/* rms_norm_forward (nn.c:169-173): y = (x * rs) * weight per row of x [..., d].
+ * On the device (needs a decoder_lm built by decoder_lm_create). */
+tensor *rms_norm_forward(struct mem_pool *scratch, rms_norm *norm, const tensor *x);
+
+/* embedding_forward (nn.c:193-199 -> tensor_embedding, embedding.c:63-110):
+ * ids [N] int32 -> rows [N, d_model] of the host table (a row copy; ids
+ * outside [0, vocab) assert).  `data` is unused, as in the reference. */
+tensor *embedding_forward(struct mem_pool *scratch, struct mem_pool *data, embedding *emb, const tensor *ids);
+
 long long linear_num_parameters(linear *l);
 long long swiglu_ffn_num_parameters(swiglu_ffn *ffn);
 long long embedding_num_parameters(embedding *emb);

@@ -28,6 +28,9 @@ tensor *tensor_scratch(struct mem_pool *pool, int ndim, const int *shape, int re
 tensor *tensor_slice(struct mem_pool *scratch, tensor *t, int dim, int start, int len);
 tensor *tensor_reshape(struct mem_pool *scratch, tensor *t, int ndim, const int *shape);
 tensor *tensor_flatten(struct mem_pool *scratch, tensor *t);
+/* a ++ b along dim (the other extents equal): a new contiguous scratch tensor
+ * (ops_elem.c:903-945, forward only). */
+tensor *tensor_cat(struct mem_pool *scratch, const tensor *a, const tensor *b, int dim);
 float  *tensor_data_ptr(tensor *t);
 int     tensor_numel(const tensor *t);
 int     tensor_ndim(const tensor *t);

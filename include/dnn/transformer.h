@@ -36,4 +36,14 @@ transformer_block *transformer_block_create(struct mem_pool *params_pool, int d_
                                             int d_k, int intermediate_size);
 long long transformer_block_num_parameters(transformer_block *block);
 
+/* Cached forward of one block over x [B, N_new, d_model] (contiguous): appends
+ * the new K/V to cache and attends over its rows (transformer.c:211-426).
+ * Runs on the device; the block must belong to a decoder_lm built by
+ * decoder_lm_create.  mode ATTENTION_PREFIX_LM needs an empty cache. */
+tensor *transformer_block_forward_cached_ex(struct mem_pool *scratch, transformer_block *block,
+                                            const tensor *x, kv_cache *cache,
+                                            attention_mode mode, int prefix_len);
+tensor *transformer_block_forward_cached(struct mem_pool *scratch, transformer_block *block,
+                                         const tensor *x, kv_cache *cache);
+
 #endif

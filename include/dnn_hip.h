@@ -141,6 +141,36 @@ int dnn_hip_prefill(dnn_hip_session *s, const float *embeds, int n_embed,
                     const int *ids, int n_ids_max, const int *n_ids,
                     int mode, int prefix_len, int *next_ids, float *logits);
 
+/* One transformer block -- layer `layer` of the model -- over n_new new rows of
+ * every batch row at positions [pos0, pos0 + n_new): transformer_block_forward_cached_ex
+ * (transformer.c:211-416) with the reference's per-layer kv_cache whose
+ * seq_len is pos0.  Appends the rows' K/V to the session's layer cache, attends
+ * over positions [0, pos0 + n_new) (mode / prefix_len as dnn_hip_prefill; mode 1
+ * needs pos0 = 0).  x and y: host [batch][n_new][d_model].  The session's
+ * lengths are not changed: the caller's cache lengths are the positions. */
+int dnn_hip_block_forward(dnn_hip_session *s, int layer, const float *x, int n_new,
+                          int pos0, int mode, int prefix_len, float *y);
+
+/* The tied lm_head over n rows x [n][d_model]: logits [n][V] = (norm ?
+ * rms_norm(x) with the final gamma : x) . embed^T + lm_head bias.  norm = 0 is
+ * decoder_lm_lm_head_forward (gpt.c:117-122); norm = 1 adds the final
+ * rms_norm_forward before it (gpt.c:357-358). */
+int dnn_hip_head_forward(dnn_hip_session *s, const float *x, int n, int norm, float *logits);
+
+/* Embedding rows of n token ids: out [n][d_model] (embedding.c:63-110; ids
+ * outside [0, V) are DNN_HIP_ERANGE, where the reference asserts). */
+int dnn_hip_embed(dnn_hip_session *s, const int *ids, int n, float *out);
+
+/* rms_norm of n rows x [n][d] with gamma [d]: y = (x * rs) * gamma, rs =
+ * 1/sqrtf(sum(x^2)/d + eps) (tensor_rms_norm, norm.c:404-495).  d <= d_model. */
+int dnn_hip_rms_norm(dnn_hip_session *s, const float *x, const float *gamma, int n, int d,
+                     float eps, float *y);
+
+/* The first len cached positions of one layer's K (which = 0) or V (which = 1)
+ * in the reference's kv_cache layout: out [batch][H][len][d_k]
+ * (kv_cache_get_K / kv_cache_get_V, transformer.c:90-112). */
+int dnn_hip_cache_read(dnn_hip_session *s, int layer, int which, int len, float *out);
+
 /* decoder_lm_generate(use_cache=1, temperature=0) for one sequence: out gets
  * prompt + generated ids (P + max_new ints), *n_out its length (stops after eos
  * when eos >= 0).  Uses a fresh session of max_seq = P + max_new. */

@@ -359,6 +359,14 @@ void orc_state_free(orc_state *s) {
 
 void orc_state_reset(orc_state *s) { s->seq_len = 0; }
 
+void orc_state_kv(const orc_state *s, int layer, int which, int len, float *out) {
+    const int H = s->m->cfg.H, dk = s->m->cfg.dk;
+    assert(len <= s->seq_len);
+    const float *src = (which ? s->v : s->k) + (size_t)layer * H * s->max_seq * dk;
+    for (int h = 0; h < H; h++)
+        memcpy(out + (size_t)h * len * dk, src + (size_t)h * s->max_seq * dk, sizeof(float) * (size_t)len * dk);
+}
+
 /* transformer_block_forward_cached_ex (transformer.c:211-416) for every layer. */
 void orc_forward_cached(orc_state *st, float *x, int N, int mode, int prefix_len) {
     const orc_model *m = st->m;

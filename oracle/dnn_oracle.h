@@ -87,6 +87,9 @@ typedef struct orc_state {
 orc_state *orc_state_create(const orc_model *m, int max_seq);
 void orc_state_free(orc_state *s);
 void orc_state_reset(orc_state *s);
+/* The first len cached rows of one layer's K (which 0) or V (which 1):
+ * out [H][len][dk] (kv_cache_get_K/V, transformer.c:102-112). */
+void orc_state_kv(const orc_state *s, int layer, int which, int len, float *out);
 
 /* transformer_block_forward_cached_ex over all layers (transformer.c:211-416) for
  * N new rows x[N][D] (overwritten by the final hidden state, before the final

@@ -57,6 +57,7 @@ def lib():
         L.orc_state_create.restype = C.c_void_p
         L.orc_state_free.argtypes = [C.c_void_p]
         L.orc_forward_cached.argtypes = [C.c_void_p, f32p, C.c_int, C.c_int, C.c_int]
+        L.orc_state_kv.argtypes = [C.c_void_p, C.c_int, C.c_int, C.c_int, f32p]
         L.orc_head.argtypes = [C.c_void_p, f32p, C.c_int, f32p]
         L.orc_embed.argtypes = [C.c_void_p, i32p, C.c_int, f32p]
         L.orc_argmax.argtypes = [f32p, C.c_int]
@@ -160,6 +161,12 @@ class State:
         x = np.ascontiguousarray(x, dtype=np.float32).copy()
         lib().orc_forward_cached(self.ptr, fp(x), x.shape[0], mode, prefix_len)
         return x
+
+    def cache(self, layer, which, length):
+        """[H][length][dk] rows of one layer's K (which 0) or V (which 1)."""
+        out = np.zeros((self.m.H, length, self.m.D // self.m.H), dtype=np.float32)
+        lib().orc_state_kv(self.ptr, layer, which, length, fp(out))
+        return out
 
     def __del__(self):
         try:

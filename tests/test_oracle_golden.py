@@ -186,3 +186,35 @@ def test_c2_first_steps_and_hashes(golden):
     toks, lg = m.generate(prompt, 4, want_logits=True)
     assert same_bits(lg, binf("c2_logits4.f32", 8192))
     assert list(toks) == golden["c2_tokens"][:36]
+
+
+def test_cache_rows_closed_form():
+    """orc_state_kv hands back layer 0's cached K/V rows as the closed form
+    fixes them: V = rms_norm(x) Wv + bv, K = RoPE_p(rms_norm(x) Wk + bk) at
+    each position p (transformer.c:223-247; fp64 here, so a tolerance), in
+    kv_cache_get_K/V order [H][len][dk]; and rows once written never change."""
+    m = O.Model(128, 256, 4, 4, 683, 64, seed=1)
+    p = m.params()
+    D, H, dk = 256, 4, 64
+    wqkv = p[1].reshape(D, 3 * D).astype(np.float64)
+    bqkv = p[2].astype(np.float64)
+    g = p[5].astype(np.float64)
+    cos, sin = m.rope_tables()
+    ids = np.array([5, 77, 3, 120, 64], dtype=np.int32)
+    x = O.embed(m, ids).astype(np.float64)
+    xn = x / np.sqrt((x * x).mean(axis=1, keepdims=True) + 1e-5) * g
+    qkv = xn @ wqkv + bqkv
+    k = qkv[:, D:2 * D].reshape(5, H, dk)
+    v = qkv[:, 2 * D:].reshape(5, H, dk)
+    c, s = cos[:5, None, :], sin[:5, None, :]
+    e, o = k[..., 0::2].copy(), k[..., 1::2].copy()
+    k[..., 0::2], k[..., 1::2] = e * c - o * s, e * s + o * c
+    st = O.State(m, 64)
+    st.forward(O.embed(m, ids[:3]))
+    k3 = st.cache(0, 0, 3)
+    st.forward(O.embed(m, ids[3:]))
+    got_k, got_v = st.cache(0, 0, 5), st.cache(0, 1, 5)
+    assert got_k.shape == (H, 5, dk)
+    np.testing.assert_allclose(got_k, k.transpose(1, 0, 2), atol=2e-5)
+    np.testing.assert_allclose(got_v, v.transpose(1, 0, 2), atol=2e-5)
+    assert same_bits(got_k[:, :3], k3)
