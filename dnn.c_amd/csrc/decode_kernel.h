@@ -44,9 +44,15 @@ struct LayerOff {
 // then the lm_head argmax partials AMAX [2][B][grid][2] (value, index), double
 // buffered by step parity: a workgroup overwrites its step-t slot at step t+2
 // only after reading every workgroup's step-(t+1) partial, each written after
-// its writer finished reading the step-t partials.
+// its writer finished reading the step-t partials.  When a head's keys are
+// split over ns > 1 workgroups, the attention partials follow, per layer:
+//   AO [B*H*ns][DK]  sum_j e^(s_j - m) v_j of record r = (b*H + h)*ns + split
+//   AML [B*H*ns][2]  (m, sum_j e^(s_j - m)) of the same record
+// and ATT is not used (the out_proj workgroups merge the records).
+constexpr int ATT_SPLIT_MAX = 4;  // workgroups per (row, head)
+constexpr int ATT_SPLIT_HEADS = 32;  // splitting needs B*H <= this (4 heads per wavefront)
 struct Exch {
-    int ldD, ldF, D, B, grid;
+    int ldD, ldF, D, B, grid, H, ns;
     __host__ __device__ size_t per_row() const { return (size_t)2 * ldD + 4 * (size_t)D + ldF; }
     __host__ __device__ size_t per_layer() const { return per_row() * B; }
     __host__ __device__ size_t base(int l, int b) const { return per_layer() * l + per_row() * b; }
@@ -60,7 +66,12 @@ struct Exch {
     __host__ __device__ size_t amax(int L, int par, int b, int g) const {
         return per_layer() * L + (((size_t)par * B + b) * grid + g) * 2;
     }
-    __host__ __device__ size_t total(int L) const { return per_layer() * L + (size_t)2 * B * grid * 2; }
+    __host__ __device__ size_t nrec() const { return ns > 1 ? (size_t)B * H * ns : 0; }
+    __host__ __device__ size_t ao(int L, int l) const {
+        return per_layer() * L + (size_t)2 * B * grid * 2 + (size_t)l * nrec() * (DK + 2);
+    }
+    __host__ __device__ size_t aml(int L, int l) const { return ao(L, l) + nrec() * DK; }
+    __host__ __device__ size_t total(int L) const { return ao(L, L); }
 };
 
 struct DecodeArgs {
@@ -90,9 +101,10 @@ struct DecodeArgs {
 
 // Dynamic LDS of the decode kernel (bytes): per-row token / position / done
 // flags, per-wavefront argmax and attention partials, the double-buffered
-// output block of a GEMV round (OUT [2][WPB][2*MAXB]), then the staged rows
+// output block of a GEMV round (OUT [2][WPB][2*MAXB]), each attention
+// wavefront's query and chunk weights (QE [WPB][DK + CH]), then the staged rows
 // XS (layer input), AS (attention), X1S and ACTS, nb rows each.
-constexpr int LDS_HEAD_WORDS = 3 * MAXB + 2 * WPB * MAXB + WPB * (DK + 2) + 2 * WPB * 2 * MAXB;
+constexpr int LDS_HEAD_WORDS = 3 * MAXB + 2 * WPB * MAXB + WPB * (DK + 2) + 2 * WPB * 2 * MAXB + WPB * (DK + CH);
 inline size_t lds_bytes(int nb, int ldD, int ldF) {
     return (size_t)4 * ((LDS_HEAD_WORDS + 3) / 4 * 4) + (size_t)4 * nb * (3 * (size_t)ldD + ldF);
 }

@@ -39,6 +39,78 @@
 
 namespace dnnhip {
 
+// DNNHIP_TRACE (timing builds only, never the product): thread 0 of every
+// workgroup stamps s_memrealtime at the phase boundaries of one chosen step
+// into trace[workgroup][layer (L = head)][event].
+#ifdef DNNHIP_TRACE
+constexpr int TRACE_L = 33, TRACE_E = 16;
+__device__ unsigned long long g_trace[256 * TRACE_L * TRACE_E];
+__device__ int g_trace_step;
+#define TRACE_EV(L_, EV)                                                                              \
+    do {                                                                                              \
+        if (tid == 0 && t == g_trace_step)                                                            \
+            g_trace[((size_t)g0 * TRACE_L + (L_)) * TRACE_E + (EV)] = __builtin_amdgcn_s_memrealtime(); \
+    } while (0)
+#else
+#define TRACE_EV(L_, EV) \
+    do {                 \
+    } while (0)
+#endif
+
+// Attention rows AS from the split records of one layer (heads split over ns
+// workgroups): record r = (b*H + h)*ns + s carries O_s = sum_j e^(s_j - m_s) v_j
+// (DK values) and (m_s, l_s = sum_j e^(s_j - m_s)); the row of head (b, h) is
+// sum_s e^(m_s - M) O_s / sum_s e^(m_s - M) l_s with M = max_s m_s -- the
+// softmax-weighted sum of transformer.c:349-397, merged from key ranges.
+// Wavefront w takes heads w, w + 8, ... (at most ATT_SPLIT_HEADS / 8 of them),
+// every record of its heads polled in one pass.
+__device__ __forceinline__ void stage_att_split(float *as, int ld, int nh, int H, int ns, size_t ao, size_t aml,
+                                                rsrc_t xa, unsigned tag, int wid, int lane, Waiter &wt) {
+    constexpr int HPW = ATT_SPLIT_HEADS / WPB;
+    u2 o[HPW][ATT_SPLIT_MAX], ml[HPW];
+    wt.reset();
+    for (;;) {
+        bool ok = true;
+#pragma unroll
+        for (int i = 0; i < HPW; i++) {
+            const int hb = wid + i * WPB;
+            if (hb >= nh) continue;
+#pragma unroll
+            for (int sp = 0; sp < ATT_SPLIT_MAX; sp++) {
+                if (sp >= ns) continue;
+                o[i][sp] = __builtin_amdgcn_raw_buffer_load_b64(
+                    xa, (unsigned)((ao + ((size_t)hb * ns + sp) * DK + lane) * 8), 0, CP_SC1);
+                ok &= o[i][sp].y == tag;
+            }
+            const int li = lane < 2 * ns ? lane : 0;
+            ml[i] = __builtin_amdgcn_raw_buffer_load_b64(xa, (unsigned)((aml + (size_t)hb * ns * 2 + li) * 8), 0, CP_SC1);
+            ok &= ml[i].y == tag;
+        }
+        if (__all(ok) || !wt.again()) break;
+    }
+#pragma unroll
+    for (int i = 0; i < HPW; i++) {
+        const int hb = wid + i * WPB;
+        if (hb >= nh) continue;
+        const float mv = as_float(ml[i].x);
+        float M = -INFINITY;
+#pragma unroll
+        for (int sp = 0; sp < ATT_SPLIT_MAX; sp++)
+            if (sp < ns) M = fmaxf(M, bcast(mv, 2 * sp));
+        float O = 0.f, den = 0.f;
+#pragma unroll
+        for (int sp = 0; sp < ATT_SPLIT_MAX; sp++) {
+            if (sp >= ns) continue;
+            const float m = bcast(mv, 2 * sp);
+            const float f = m == -INFINITY ? 0.f : expf(m - M);
+            O += f * as_float(o[i][sp].x);
+            den += f * bcast(mv, 2 * sp + 1);
+        }
+        const int b = hb / H, h = hb - b * H;
+        as[b * ld + h * DK + lane] = O / den;
+    }
+}
+
 // The decode loop of one session on workgroups g0 = 0 .. G-1.
 template <int NB, int DC>
 __device__ __forceinline__ void decode_v3_body(const DecodeArgs &a, const int G, const int g0) {
@@ -50,6 +122,7 @@ __device__ __forceinline__ void decode_v3_body(const DecodeArgs &a, const int G,
     int *s_bi = reinterpret_cast<int *>(s_bv + WPB * MAXB);     // [WPB][MAXB]
     float *s_part = reinterpret_cast<float *>(s_bi + WPB * MAXB);   // [WPB][DK + 2]
     float *s_out = s_part + WPB * (DK + 2);                     // [2][WPB][2 * MAXB]
+    float *s_qe = s_out + 2 * WPB * 2 * MAXB;                   // [WPB][DK + CH]
     const int ldD = a.ldD, ldF = a.ldF;
     float *xs = smem + (LDS_HEAD_WORDS + 3) / 4 * 4;            // [NB][ldD] layer input (raw)
     float *as = xs + NB * ldD;                                  // [NB][ldD] attention output
@@ -63,6 +136,7 @@ __device__ __forceinline__ void decode_v3_body(const DecodeArgs &a, const int G,
     const int nw = G * WPB;
     const int B = a.B, D = a.D, H = a.H, F = a.F, V = a.V;
     const int nrows = B < NB ? B : NB;
+    const int ns = a.ex.ns > 1 ? a.ex.ns : 1;                  // workgroups per (row, head)
     Waiter wt{a.err};
 
     const size_t kv_head = (size_t)DK * a.max_seq;              // floats per (layer, row, head)
@@ -92,6 +166,7 @@ __device__ __forceinline__ void decode_v3_body(const DecodeArgs &a, const int G,
         __syncthreads();
 
         for (int l = 0; l < a.L; l++) {
+            TRACE_EV(l, 0);
             const LayerOff w = load_layer(a.layers + l);
             // opaque per layer: keeps the compiler from hoisting every phase's
             // lane-dependent addresses out of the loops (they would all stay
@@ -152,6 +227,7 @@ __device__ __forceinline__ void decode_v3_body(const DecodeArgs &a, const int G,
                     stage_rows<NB * 6 / WPB + 1>(xs, ldD, D, nrows, a.ex.x2(l - 1, 0), xstride, xa, tag, wid, lane, wt);
                 }
                 __syncthreads();
+                TRACE_EV(l, 1);
                 if (busy) {
                     float rs[NB];
                     rms_lds<NB, DC>(xs, ldD, D, w.eps_attn, lane, rs);
@@ -168,12 +244,17 @@ __device__ __forceinline__ void decode_v3_body(const DecodeArgs &a, const int G,
                 }
             }
 
-            // ---- B: attention of (row b, head h) = workgroup G-1-((b*H + h) mod G):
-            // the last workgroups, which hold no phase-A units for the model
-            // shapes served, so their K/V loads start as the layer starts.
-            // Scores: lanes 0-31 hold dims 0-31, lanes 32-63 dims 32-63 of the
-            // chunk's 32 keys (key = j0 + (lane & 31)); P.V: lane = output dim.
-            for (int bh = G - 1 - g0; bh < B * H; bh += G) {
+            TRACE_EV(l, 2);
+            // ---- B: attention.  Record r = (b*H + h)*ns + split runs on workgroup
+            // G-1-(r mod G): the last workgroups, which hold no phase-A units for
+            // the model shapes served, so their K/V loads start as the layer
+            // starts.  Split sp takes the 32-key chunks c = sp + ns*(w + 8k)
+            // (wavefront w).  Scores: lanes 0-31 hold dims 0-31, lanes 32-63 dims
+            // 32-63 of the chunk's 32 keys (key = j0 + (lane & 31)); P.V: lane =
+            // output dim.  One split (ns = 1) writes the head's ATT row; more
+            // write (O, m, l) records that phase C merges.
+            for (int r = G - 1 - g0; r < B * H * ns; r += G) {
+                const int bh = r / ns, sp = r - bh * ns;
                 const int b = bh / H, h = bh - b * H;
                 const int p = s_pos[b], S = p + 1, nch = (S + CH - 1) / CH;
                 const int half = lane >> 5, kl = lane & 31;
@@ -181,7 +262,7 @@ __device__ __forceinline__ void decode_v3_body(const DecodeArgs &a, const int G,
                 float m_run = -INFINITY, l_run = 0.f, o_run = 0.f;
                 float q = 0.f, kn = 0.f, vn = 0.f;
                 bool have_q = false;
-                for (int c = wid; c < nch; c += WPB) {
+                for (int c = sp + ns * wid; c < nch; c += ns * WPB) {
                     const int j0 = c * CH, key = j0 + kl;
                     // cached keys (positions < p) of this chunk, issued before the waits
                     // (unconditional loads, then a select: keys >= p hold stale or
@@ -199,23 +280,48 @@ __device__ __forceinline__ void decode_v3_body(const DecodeArgs &a, const int G,
                         const float tv = ld1s<CP_SC1>(rv, vvo, (unsigned)(jj * DK * 4));
                         vr[jj] = j0 + jj < p ? tv : 0.f;
                     }
-                    if (!have_q) { q = poll1(xa, (long)(a.ex.q(l, b) + h * DK + lane), tag, wt); have_q = true; }
-                    asm volatile("" : "+v"(q));     // no hoisting of the per-half q selects below
                     const bool has_new = p >= j0 && p < j0 + CH;
+                    if (!have_q || has_new) {
+                        // this step's q (first chunk) and new k, v (the chunk
+                        // holding position p), polled together: one hop
+                        const size_t qp = a.ex.q(l, b) + h * DK + lane;
+                        const bool wq = !have_q;
+                        wt.reset();
+                        for (;;) {
+                            u2 v0 = {0u, tag}, v1 = {0u, tag}, v2 = {0u, tag};
+                            if (wq) v0 = __builtin_amdgcn_raw_buffer_load_b64(xa, (unsigned)(qp * 8), 0, CP_SC1);
+                            if (has_new) {
+                                v1 = __builtin_amdgcn_raw_buffer_load_b64(xa, (unsigned)((qp + D) * 8), 0, CP_SC1);
+                                v2 = __builtin_amdgcn_raw_buffer_load_b64(xa, (unsigned)((qp + 2 * D) * 8), 0, CP_SC1);
+                            }
+                            if (wq) q = as_float(v0.x);
+                            kn = as_float(v1.x);
+                            vn = as_float(v2.x);
+                            if (__all(v0.y == tag && v1.y == tag && v2.y == tag) || !wt.again()) break;
+                        }
+                        have_q = true;
+                        TRACE_EV(l, 9);
+                    }
+                    asm volatile("" : "+v"(q));     // no hoisting of the per-half q selects below
                     if (has_new) {
-                        kn = poll1(xa, (long)(a.ex.kn(l, b) + h * DK + lane), tag, wt);
-                        vn = poll1(xa, (long)(a.ex.vn(l, b) + h * DK + lane), tag, wt);
-                        // append position p to the caches and wait until the stores
-                        // are complete (device scope): __syncthreads does not wait
-                        // for vector memory, so this orders them before the ATT
-                        // store below and every later step's reads
+                        // append position p to the caches (transformer.c:76-93); the
+                        // stores are waited for (device scope) before the workgroup
+                        // leaves the head, so they complete before any later step
+                        // reads position p
                         st1(rk, (head + (size_t)lane * a.max_seq + p) * 4, kn);    // K^T[d][p]
                         st1(rv, (head + (size_t)p * DK + lane) * 4, vn);           // V[p][d]
-                        __builtin_amdgcn_s_waitcnt(0x0f70);                       // vmcnt(0)
                     }
+                    // q and the chunk's weights go through this wavefront's QE slot
+                    // (16-byte LDS reads that every lane of a half-wave shares):
+                    // no per-lane selects between broadcast registers
+                    float *qe = s_qe + wid * (DK + CH);
+                    qe[lane] = q;
                     float s = 0.f;
 #pragma unroll
-                    for (int i = 0; i < 32; i++) s += (half ? bcast(q, 32 + i) : bcast(q, i)) * kt[i];
+                    for (int i = 0; i < 32; i += 4) {
+                        const f4 qv = *reinterpret_cast<const f4 *>(qe + 32 * half + i);
+                        s += qv.x * kt[i] + qv.y * kt[i + 1] + qv.z * kt[i + 2] + qv.w * kt[i + 3];
+                    }
                     s += __shfl_xor(s, 32, WAVE);                              // transformer.c:291-297
                     s = s * scale;
                     if (has_new) {
@@ -227,17 +333,26 @@ __device__ __forceinline__ void decode_v3_body(const DecodeArgs &a, const int G,
                     const float m_new = fmaxf(m_run, m_c);
                     const float e = valid ? expf(s - m_new) : 0.f;
                     const float fa = expf(m_run - m_new);
+                    if (lane < CH) qe[DK + lane] = e;
                     float o = 0.f;
 #pragma unroll
-                    for (int jj = 0; jj < CH; jj++) o += bcast(e, jj) * vr[jj];
+                    for (int jj = 0; jj < CH; jj += 4) {
+                        const f4 ev = *reinterpret_cast<const f4 *>(qe + DK + jj);
+                        o += ev.x * vr[jj] + ev.y * vr[jj + 1] + ev.z * vr[jj + 2] + ev.w * vr[jj + 3];
+                    }
                     if (has_new) o += bcast(e, p - j0) * vn;
                     l_run = l_run * fa + wave_sum(half ? 0.f : e);
                     o_run = o_run * fa + o;
                     m_run = m_new;
                 }
+                // a split whose first wavefront has no chunk still waits for this
+                // step's query, so its record is never written ahead of the step
+                if (!have_q && wid == 0) (void)poll1(xa, (long)(a.ex.q(l, b) + h * DK + lane), tag, wt);
                 s_part[wid * (DK + 2) + lane] = o_run;
                 if (lane == 0) { s_part[wid * (DK + 2) + DK] = m_run; s_part[wid * (DK + 2) + DK + 1] = l_run; }
+                TRACE_EV(l, 10);
                 __syncthreads();
+                TRACE_EV(l, 11);
                 if (wid == 0) {
                     float M = -INFINITY;
                     for (int ww = 0; ww < WPB; ww++) M = fmaxf(M, s_part[ww * (DK + 2) + DK]);
@@ -248,11 +363,18 @@ __device__ __forceinline__ void decode_v3_body(const DecodeArgs &a, const int G,
                         O += s_part[ww * (DK + 2) + lane] * f;
                         Ls += s_part[ww * (DK + 2) + DK + 1] * f;
                     }
-                    put(xa, a.ex.att(l, b) + h * DK + lane, O / Ls, tag);
+                    if (ns == 1) {
+                        put(xa, a.ex.att(l, b) + h * DK + lane, O / Ls, tag);
+                    } else {
+                        put(xa, a.ex.ao(a.L, l) + (size_t)r * DK + lane, O, tag);
+                        if (lane < 2) put(xa, a.ex.aml(a.L, l) + (size_t)r * 2 + lane, lane == 0 ? M : Ls, tag);
+                    }
                 }
+                __builtin_amdgcn_s_waitcnt(0x0f70);                           // vmcnt(0): cache appends done
                 __syncthreads();
             }
 
+            TRACE_EV(l, 3);
             // ---- C: out_proj + bias + residual -> X1 (transformer.c:408); unit u =
             // rows (2u, 2u+1), workgroup-contiguous rounds as in A
             {
@@ -280,9 +402,14 @@ __device__ __forceinline__ void decode_v3_body(const DecodeArgs &a, const int G,
                 for (int k = 0; k < UP; k++)
                     if ((k * G + g0) * WPB + wid < nu) load_c(k, (k * G + g0) * WPB + wid);
                 const bool busy = g0 * WPB < nu;
-                if (busy)
-                    stage_rows<NB * 6 / WPB + 1>(as, ldD, D, nrows, a.ex.att(l, 0), xstride, xa, tag, wid, lane, wt);
+                if (busy) {
+                    if (ns == 1)
+                        stage_rows<NB * 6 / WPB + 1>(as, ldD, D, nrows, a.ex.att(l, 0), xstride, xa, tag, wid, lane, wt);
+                    else
+                        stage_att_split(as, ldD, B * H, H, ns, a.ex.ao(a.L, l), a.ex.aml(a.L, l), xa, tag, wid, lane, wt);
+                }
                 __syncthreads();
+                TRACE_EV(l, 4);
                 if (busy) {
                     for (int k = 0; (k * G + g0) * WPB < nu; k++) {
                         const int u0 = (k * G + g0) * WPB, u = u0 + wid;
@@ -297,6 +424,7 @@ __device__ __forceinline__ void decode_v3_body(const DecodeArgs &a, const int G,
                 }
             }
 
+            TRACE_EV(l, 5);
             // ---- D: rms_norm(X1) -> gate/up + bias -> SwiGLU -> ACT  (nn.c:61-78,
             // simd.h:394-397); unit f = gate row f and up row f
             {
@@ -327,6 +455,7 @@ __device__ __forceinline__ void decode_v3_body(const DecodeArgs &a, const int G,
                 if (busy || g0 * WPB < D)            // phase E reads X1S for its residual
                     stage_rows<NB * 6 / WPB + 1>(x1s, ldD, D, nrows, a.ex.x1(l, 0), xstride, xa, tag, wid, lane, wt);
                 __syncthreads();
+                TRACE_EV(l, 6);
                 if (busy) {
                     float rs[NB];
                     rms_lds<NB, DC>(x1s, ldD, D, w.eps_ffn, lane, rs);
@@ -343,6 +472,7 @@ __device__ __forceinline__ void decode_v3_body(const DecodeArgs &a, const int G,
                 }
             }
 
+            TRACE_EV(l, 7);
             // ---- E: down + bias + residual -> X2 (transformer.c:415); unit n = row n
             {
                 const int nu = D, FC = ldF / 256;
@@ -359,6 +489,7 @@ __device__ __forceinline__ void decode_v3_body(const DecodeArgs &a, const int G,
                 if (busy)
                     stage_rows<NB * 16 / WPB + 1>(acts, ldF, F, nrows, a.ex.act(l, 0), xstride, xa, tag, wid, lane, wt);
                 __syncthreads();
+                TRACE_EV(l, 8);
                 if (busy) {
                     for (int k = 0; (k * G + g0) * WPB < nu; k++) {
                         const int u0 = (k * G + g0) * WPB, n = u0 + wid;
@@ -385,10 +516,11 @@ __device__ __forceinline__ void decode_v3_body(const DecodeArgs &a, const int G,
             }
         }
 
+        TRACE_EV(a.L, 0);
         // ---- F: final rms_norm -> tied lm_head + bias -> per-workgroup argmax
         asm volatile("" : "+v"(lane));
         {
-            constexpr int UP = 4;
+            constexpr int UP = 1;
             float bv[NB];
             int bi[NB];
 #pragma unroll
@@ -414,20 +546,18 @@ __device__ __forceinline__ void decode_v3_body(const DecodeArgs &a, const int G,
                         a.logits[((size_t)t * B + b) * V + v + lane] = lane == 0 ? l0 : l1;
                 }
             };
-#pragma unroll
-            for (int k = 0; k < UP; k++)
-                if (gw + k * nw < nu) load_f(k, gw + k * nw);
             if (gw < nu) load_gamma<DC>(g, rw, a.g_final, lane);
             if (g0 < nu)
                 stage_rows<NB * 6 / WPB + 1>(xs, ldD, D, nrows, a.ex.x2(a.L - 1, 0), xstride, xa, tag, wid, lane, wt);
             __syncthreads();
+            TRACE_EV(a.L, 1);
             if (gw < nu) {
+                // the rows are loaded after the wait, one unit at a time: more
+                // rows in registers, or rows held across the polling loop, are
+                // spilled here, one load at a time
                 float rs[NB];
                 rms_lds<NB, DC>(xs, ldD, D, a.eps_final, lane, rs);
-#pragma unroll
-                for (int k = 0; k < UP; k++)
-                    if (gw + k * nw < nu) comp_f(k, gw + k * nw, rs);
-                for (int u = gw + UP * nw; u < nu; u += nw) {
+                for (int u = gw; u < nu; u += nw) {
                     load_f(0, u);
                     comp_f(0, u, rs);
                 }
@@ -437,6 +567,7 @@ __device__ __forceinline__ void decode_v3_body(const DecodeArgs &a, const int G,
                 for (int b = 0; b < NB; b++) { s_bv[wid * MAXB + b] = bv[b]; s_bi[wid * MAXB + b] = bi[b]; }
             }
             __syncthreads();
+            TRACE_EV(a.L, 2);
             if (tid < B) {
                 float v = -INFINITY;
                 int i = 0x7fffffff;
@@ -456,19 +587,28 @@ __device__ __forceinline__ void decode_v3_body(const DecodeArgs &a, const int G,
         for (int b = wid; b < B; b += WPB) {
             float v = -INFINITY;
             int i = 0x7fffffff;
-            for (int gb = 0; gb < G; gb += WAVE) {
-                const int gg = gb + lane;
-                const size_t pa = a.ex.amax(a.L, t & 1, b, gg < G ? gg : 0);
-                u4 q;
+            // every workgroup's partial in one polling pass (4 per lane)
+            for (int gb = 0; gb < G; gb += 4 * WAVE) {
+                u4 q[4];
                 wt.reset();
                 for (;;) {
-                    q = __builtin_amdgcn_raw_buffer_load_b128(xa, (unsigned)(pa * 8), 0, CP_SC1);
-                    const unsigned t0 = q.y, t1 = q.w;
-                    if (__all(t0 == tag && t1 == tag) || !wt.again()) break;
+                    bool ok = true;
+#pragma unroll
+                    for (int k = 0; k < 4; k++) {
+                        const int gg = gb + k * WAVE + lane;
+                        const size_t pa = a.ex.amax(a.L, t & 1, b, gg < G ? gg : 0);
+                        q[k] = __builtin_amdgcn_raw_buffer_load_b128(xa, (unsigned)(pa * 8), 0, CP_SC1);
+                        ok &= q[k].y == tag && q[k].w == tag;
+                    }
+                    if (__all(ok) || !wt.again()) break;
                 }
-                const float vv = as_float(q.x);
-                const int ii = (int)(unsigned)q.z;
-                if (gg < G && (vv > v || (vv == v && ii < i))) { v = vv; i = ii; }
+#pragma unroll
+                for (int k = 0; k < 4; k++) {
+                    const int gg = gb + k * WAVE + lane;
+                    const float vv = as_float(q[k].x);
+                    const int ii = (int)(unsigned)q[k].z;
+                    if (gg < G && (vv > v || (vv == v && ii < i))) { v = vv; i = ii; }
+                }
             }
 #pragma unroll
             for (int o = 32; o >= 1; o >>= 1) {
@@ -485,6 +625,7 @@ __device__ __forceinline__ void decode_v3_body(const DecodeArgs &a, const int G,
             }
         }
         __syncthreads();
+        TRACE_EV(a.L, 3);
         if (a.eos >= 0) {
             int all = 1;
             for (int b = 0; b < B; b++) all &= s_done[b];
@@ -506,6 +647,18 @@ DNNHIP_INST(1, 1) DNNHIP_INST(1, 2) DNNHIP_INST(1, 3)
 DNNHIP_INST(2, 1) DNNHIP_INST(2, 2) DNNHIP_INST(2, 3)
 DNNHIP_INST(4, 1) DNNHIP_INST(4, 2) DNNHIP_INST(4, 3)
 DNNHIP_INST(8, 1) DNNHIP_INST(8, 2) DNNHIP_INST(8, 3)
+
+#ifdef DNNHIP_TRACE
+extern "C" int dnn_hip_trace_arm(int step) {
+    static unsigned long long zero[256 * TRACE_L * TRACE_E];
+    if (hipMemcpyToSymbol(HIP_SYMBOL(g_trace), zero, sizeof zero) != hipSuccess) return -1;
+    return hipMemcpyToSymbol(HIP_SYMBOL(g_trace_step), &step, sizeof step) == hipSuccess ? 0 : -1;
+}
+extern "C" int dnn_hip_trace_read(unsigned long long *out) {
+    return hipMemcpyFromSymbol(out, HIP_SYMBOL(g_trace), sizeof(unsigned long long) * 256 * TRACE_L * TRACE_E) ==
+                   hipSuccess ? 0 : -1;
+}
+#endif
 
 const void *decode_kernel_for(int nb, int dc) {
 #define DNNHIP_PICK(NB, DC) if (nb == NB && dc == DC) return reinterpret_cast<const void *>(&decode_v3<NB, DC>);

@@ -321,12 +321,14 @@ int dnn_hip_session_create(dnn_hip_model *m, int B, int max_seq, dnn_hip_session
     s->kv_s = (int)round_up((size_t)max_seq, BK_SEQ_ALIGN);
     s->h_pos.assign(B, 0);
     if (const char *k = getenv("DNN_HIP_DECODE_KERNEL")) s->kernel_pref = atoi(k);
+    if (const char *k = getenv("DNN_HIP_ATT_SPLITS")) s->att_splits_req = atoi(k);
     // more than MAXB rows, bf16 weights, or on request: the batched engine
     s->batched = B > MAXB || m->bf16 || s->kernel_pref == 6;
     int n_cu = 0;
     if (hipDeviceGetAttribute(&n_cu, hipDeviceAttributeMultiprocessorCount, m->device) != hipSuccess || n_cu <= 0) n_cu = 256;
     s->grid_cap = n_cu;
-    s->ex = Exch{m->ldD, m->ldF, m->D, B, s->grid_cap};
+    // room for heads split over up to ATT_SPLIT_MAX workgroups when B*H allows it
+    s->ex = Exch{m->ldD, m->ldF, m->D, B, s->grid_cap, m->H, B * m->H <= ATT_SPLIT_HEADS ? ATT_SPLIT_MAX : 1};
     // the kernels read whole 64-key chunks: the row stride kv_s covers them
     const size_t kv = (size_t)m->L * B * m->H * s->kv_s * DK + (size_t)CH * DK;
     size_t xa_pairs = s->batched ? 1 : s->ex.total(m->L);
@@ -414,6 +416,12 @@ int dnn_hip_session_kernel(dnn_hip_session *s, int *which) {
     return DNN_HIP_OK;
 }
 
+int dnn_hip_session_att_splits(dnn_hip_session *s, int *splits) {
+    if (!s || !splits) return fail(DNN_HIP_EINVAL, "NULL argument");
+    *splits = s->att_splits;
+    return DNN_HIP_OK;
+}
+
 int dnn_hip_session_last_ms(dnn_hip_session *s, float *ms) {
     if (!s || !ms) return fail(DNN_HIP_EINVAL, "NULL argument");
     *ms = s->last_ms;
@@ -448,6 +456,27 @@ int dnnhip::check_decode(dnn_hip_session *s, const int *feed, int n_feed_all, co
 }  // extern "C++"
 
 namespace {
+
+// Workgroups per (row, head) of decode_v3's attention in a launch of n_steps:
+// enough that each wavefront walks at most 4 32-key chunks of the longest
+// history the launch reaches (measured on the C2 shape: a split costs the
+// out_proj workgroups more staging than it saves below that), no more than the
+// workgroups idle during the QKV phase (so every split starts its key loads
+// with the layer), and at most ATT_SPLIT_MAX; DNN_HIP_ATT_SPLITS fixes it
+// instead.
+int att_splits(const dnn_hip_session *s, int grid, int n_steps) {
+    const dnn_hip_model *m = s->m;
+    const int heads = s->B * m->H;
+    if (s->ex.ns <= 1) return 1;
+    if (s->att_splits_req > 0) return std::min(s->att_splits_req, s->ex.ns);
+    int pmax = 0;
+    for (int b = 0; b < s->B; b++) pmax = std::max(pmax, s->h_pos[b] + n_steps);
+    const int nch = (pmax + CH - 1) / CH;
+    const int idle = grid - std::min(grid, (3 * m->D / 2 + WPB - 1) / WPB);
+    int ns = std::min(s->ex.ns, (nch + 4 * WPB - 1) / (4 * WPB));
+    while (ns > 1 && heads * ns > idle) ns--;
+    return std::max(ns, 1);
+}
 
 // Validate and enqueue one launch of a persistent decode kernel on the
 // session's stream; decode_finish waits for it.
@@ -525,6 +554,8 @@ int decode_launch(dnn_hip_session *s, const int *feed, int n_feed_all, const int
     a.B = B; a.max_seq = s->kv_s;
     a.kc = s->kc; a.vc = s->vc; a.xa = s->xa; a.ex = s->ex;
     a.ex.grid = s->grid_cap;
+    a.ex.ns = s->kernel_used == 3 ? att_splits(s, grid, n_steps) : 1;
+    s->att_splits = a.ex.ns;
     a.pos = s->pos; a.feed = s->feed; a.n_feed = s->n_feed;
     a.ids = s->ids; a.logits = want_logits ? s->logits : nullptr;
     a.n_steps = n_steps; a.eos = eos; a.step0 = s->next_tag; a.err = s->err; a.steps_done = s->steps_done;

@@ -23,7 +23,7 @@ HIP_SYMBOLS = [
     "dnn_hip_model_rope", "dnn_hip_model_destroy", "dnn_hip_session_create",
     "dnn_hip_session_reset", "dnn_hip_session_lengths", "dnn_hip_session_destroy",
     "dnn_hip_decode", "dnn_hip_generate", "dnn_hip_session_last_ms", "dnn_hip_session_set_grid",
-    "dnn_hip_session_grid", "dnn_hip_session_kernel", "dnn_hip_model_create_ex", "dnn_hip_prefill",
+    "dnn_hip_session_grid", "dnn_hip_session_kernel", "dnn_hip_session_att_splits", "dnn_hip_model_create_ex", "dnn_hip_prefill",
     "dnn_hip_block_forward", "dnn_hip_head_forward", "dnn_hip_embed", "dnn_hip_cache_read", "dnn_hip_rms_norm",
 ]
 
@@ -61,6 +61,7 @@ def hip():
         L.dnn_hip_session_set_grid.argtypes = [C.c_void_p, C.c_int]
         L.dnn_hip_session_grid.argtypes = [C.c_void_p, i32p]
         L.dnn_hip_session_kernel.argtypes = [C.c_void_p, i32p]
+        L.dnn_hip_session_att_splits.argtypes = [C.c_void_p, i32p]
         L.dnn_hip_model_create_ex.argtypes = [C.c_int] * 6 + [C.POINTER(f32p), C.c_int, f32p, C.c_int,
                                                               C.POINTER(C.c_void_p)]
         L.dnn_hip_prefill.argtypes = [C.c_void_p, f32p, C.c_int, i32p, C.c_int, i32p, C.c_int, C.c_int, i32p, f32p]
@@ -138,6 +139,12 @@ class HipSession:
         """3..6: the decode kernel of the last decode() call (6: the batched engine)."""
         k = C.c_int()
         check(hip().dnn_hip_session_kernel(self.ptr, C.byref(k)))
+        return k.value
+
+    def att_splits(self):
+        """Workgroups per (row, head) of the last general-kernel launch's attention."""
+        k = C.c_int()
+        check(hip().dnn_hip_session_att_splits(self.ptr, C.byref(k)))
         return k.value
 
     def set_grid(self, n):

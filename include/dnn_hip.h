@@ -194,6 +194,11 @@ int dnn_hip_session_grid(dnn_hip_session *s, int *n_workgroups);
  * schedule fits the model and grid; 6 = the batched engine (more than 8 rows,
  * bf16 weights, or DNN_HIP_DECODE_KERNEL=6). */
 int dnn_hip_session_kernel(dnn_hip_session *s, int *which);
+/* Workgroups per (row, head) over which the last general-kernel (3) launch split
+ * each head's cached keys (1 = unsplit; chosen from the launch's longest
+ * history, or fixed by the environment variable DNN_HIP_ATT_SPLITS at session
+ * creation). */
+int dnn_hip_session_att_splits(dnn_hip_session *s, int *splits);
 
 #ifdef __cplusplus
 }
