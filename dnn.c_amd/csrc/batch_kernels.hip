@@ -43,7 +43,6 @@ namespace dnnhip {
 namespace {
 
 constexpr int NTHR = 256;
-constexpr int ATHR = 256;                              // decode attention: four wavefronts
 
 __device__ __forceinline__ f4 mfma4(float a, float b, f4 c) {
     return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
@@ -552,13 +551,13 @@ __global__ __launch_bounds__(FIN_THR) void head_finish_kernel(const GemmArgs g) 
 // ---------------------------------------------------------------------------
 // Decode attention.  Workgroup (row m, head h, split s) takes the 64-key chunks
 // c = s (mod nsplit) of the row's S = pos[m] + 1 cached keys; wavefront w the
-// chunks with c / nsplit = w (mod 4).  Lane l holds keys 64c + 4(l%16) + 0..3
+// chunks with c / nsplit = w (mod AW).  Lane l holds keys 64c + 4(l%16) + 0..3
 // for the scores (dims l/16 + 4i from K^T, summed over the four lane groups),
 // and dims 4(l%16) + 0..3 of keys 64c + l/16 + 4i for P.V.  Running max /
 // sum per wavefront (transformer.c:354-359), merged across wavefronts in LDS
 // and across splits by the last workgroup of the (row, head).
-__global__ __launch_bounds__(ATHR) void attn_kernel(const AttnArgs a) {
-    constexpr int AW = ATHR / 64;                     // wavefronts
+template <int AW>
+__global__ __launch_bounds__(64 * AW) void attn_kernel(const AttnArgs a) {
     __shared__ float s_p[AW][64];
     __shared__ float s_o[AW][BK_DK];
     __shared__ float s_ml[AW][2];
@@ -582,6 +581,10 @@ __global__ __launch_bounds__(ATHR) void attn_kernel(const AttnArgs a) {
 #pragma unroll
     for (int i = 0; i < 16; i++) qv[i] = a.q[(size_t)m * a.D + h * BK_DK + q4 + 4 * i];
     const int c0 = sp + a.nsplit * w;
+    // wavefronts 0-3 load their first chunk before the row's length is known
+    // (keys 0-255 of a split: most rows have them); the others wait for it, so
+    // short rows do not fetch keys they never use
+    const bool spec = w < 4;
     f4 kt[16], vv[16];
     auto load_chunk = [&](int c) {
         const int j0 = 64 * c;
@@ -592,7 +595,7 @@ __global__ __launch_bounds__(ATHR) void attn_kernel(const AttnArgs a) {
         for (int i = 0; i < 16; i++)
             vv[i] = lda4(rv, (unsigned)((((size_t)(j0 + q4 + 4 * i)) * BK_DK + 4 * r16) * 4));
     };
-    load_chunk(c0);
+    if (spec) load_chunk(c0);
     __builtin_amdgcn_sched_barrier(0);
     if (done) return;
     const int S = posm + 1;
@@ -602,7 +605,7 @@ __global__ __launch_bounds__(ATHR) void attn_kernel(const AttnArgs a) {
     f4 o = {0.f, 0.f, 0.f, 0.f};
     for (int c = c0; c < nch; c += AW * a.nsplit) {
         const int j0 = 64 * c;
-        if (c != c0) load_chunk(c);
+        if (c != c0 || !spec) load_chunk(c);
         f4 s = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
         for (int i = 0; i < 16; i++) {
@@ -957,7 +960,13 @@ hipError_t launch_head_finish(const GemmArgs &g, hipStream_t stream) {
 }
 
 hipError_t launch_attn(const AttnArgs &a, hipStream_t stream) {
-    hipLaunchKernelGGL(attn_kernel, dim3(a.M * a.H * a.nsplit), dim3(ATHR), 0, stream, a);
+    // eight wavefronts per (row, head, split) when there are few of them (one
+    // workgroup per CU at this register use: every chunk of up to 512 keys in
+    // one round), four otherwise (two workgroups per CU)
+    if (a.M * a.H <= 128)
+        hipLaunchKernelGGL(attn_kernel<8>, dim3(a.M * a.H * a.nsplit), dim3(512), 0, stream, a);
+    else
+        hipLaunchKernelGGL(attn_kernel<4>, dim3(a.M * a.H * a.nsplit), dim3(256), 0, stream, a);
     return hipGetLastError();
 }
 
