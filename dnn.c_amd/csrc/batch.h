@@ -50,6 +50,8 @@ struct GemmArgs {
     int lda, M, mpad;           // mpad: rows the A buffer holds (loads past it read 0)
     const void *W;              // fp32 or bf16 elements
     size_t w_bytes;             // bytes from W to the end of its arena (loads past it read 0)
+    const void *Wp;             // the same matrix in fragment order (decode shape), or null
+    size_t wp_bytes;            // bytes of the packed matrix
     int ldw, N, K;
     int ks;                     // workgroups per column tile (split K), >= 1
     int mt_max;                 // decode shape: at most this many 16-row tiles per workgroup (0: all rows)
@@ -134,6 +136,9 @@ struct EmbedArgs {
 
 // host-side launchers (batch_kernels.hip); all enqueue on `stream` and return
 // a hipError_t.  bf16: W holds bf16 weights.
+// W (N rows of ld elements, fp32 or bf16) -> dst in fragment order
+// [ceil(N/16)][ld/16][64][4], rows past N zero.
+hipError_t launch_pack(const void *W, void *dst, int N, int ld, bool bf16, hipStream_t stream);
 hipError_t launch_gemm(int epi, bool norm, bool bf16, bool prefill, const GemmArgs &g, hipStream_t stream);
 hipError_t launch_head_finish(const GemmArgs &g, hipStream_t stream);
 hipError_t launch_attn(const AttnArgs &a, hipStream_t stream);

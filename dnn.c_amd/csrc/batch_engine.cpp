@@ -85,8 +85,54 @@ void drop_graph(BatchEngine *e) {
 }
 
 // The session's engine with activation buffers of at least `rows` rows.
+// The fragment-ordered weight copy the decode GEMMs read (built on the
+// device from the arena at first use and after every weight upload).
+int ensure_packed(dnn_hip_model *m, hipStream_t stream) {
+    if (m->packed_valid) return DNN_HIP_OK;
+    const size_t es = m->bf16 ? 2 : 4;
+    auto elems = [](int N, int ld) { return (size_t)((N + 15) / 16) * 16 * (size_t)ld; };
+    const int D = m->D, F = m->F, ldD = m->ldD, ldF = m->ldF;
+    size_t o = 0;
+    m->pk_embed = o;
+    o += elems(m->V, ldD);
+    m->pk_l.assign((size_t)m->L * 4, 0);
+    for (int l = 0; l < m->L; l++) {
+        size_t *p = &m->pk_l[(size_t)l * 4];
+        p[0] = o; o += elems(3 * D, ldD);
+        p[1] = o; o += elems(D, ldD);
+        p[2] = o; o += elems(2 * F, ldD);
+        p[3] = o; o += elems(D, ldF);
+    }
+    if (!m->packed || m->packed_bytes != o * es) {
+        if (m->packed) (void)hipFree(m->packed);
+        m->packed = nullptr;
+        const hipError_t e = hipMalloc(&m->packed, o * es);
+        if (e != hipSuccess) return set_error(DNN_HIP_ENOMEM, "hipMalloc(%zu) for the packed weights: %s", o * es, hipGetErrorString(e));
+        m->packed_bytes = o * es;
+    }
+    const char *src = m->bf16 ? reinterpret_cast<const char *>(m->arena16) : m->arena;
+    char *dst = static_cast<char *>(m->packed);
+    const bool bf = m->bf16 != 0;
+    HIP_TRY(launch_pack(src + m->off.embed / 4 * es, dst + m->pk_embed * es, m->V, ldD, bf, stream));
+    for (int l = 0; l < m->L; l++) {
+        const LayerOff &lo = m->h_layers[l];
+        const size_t *p = &m->pk_l[(size_t)l * 4];
+        HIP_TRY(launch_pack(src + (size_t)lo.wqkv * es, dst + p[0] * es, 3 * D, ldD, bf, stream));
+        HIP_TRY(launch_pack(src + (size_t)lo.wo * es, dst + p[1] * es, D, ldD, bf, stream));
+        HIP_TRY(launch_pack(src + (size_t)lo.wgu * es, dst + p[2] * es, 2 * F, ldD, bf, stream));
+        HIP_TRY(launch_pack(src + (size_t)lo.wd * es, dst + p[3] * es, D, ldF, bf, stream));
+    }
+    HIP_TRY(hipStreamSynchronize(stream));
+    m->packed_valid = true;
+    return DNN_HIP_OK;
+}
+
 int engine_get(dnn_hip_session *s, int rows) {
     dnn_hip_model *m = s->m;
+    {
+        const int rc = ensure_packed(m, s->stream);
+        if (rc) return rc;
+    }
     if (m->L * 5 + 1 >= 128) return set_error(DNN_HIP_EINVAL, "%d layers: the batched engine covers up to 25", m->L);
     if (m->H > 64) return set_error(DNN_HIP_EINVAL, "%d heads: the batched engine covers up to 64", m->H);
     if (m->V > 65535) return set_error(DNN_HIP_EINVAL, "vocab %d: the batched engine covers up to 65535", m->V);
@@ -162,10 +208,13 @@ struct Wts {
     }
 };
 
-GemmArgs gemm_base(dnn_hip_session *s, const Wts &W, uint32_t woff, int ldw, int N, int K) {
+GemmArgs gemm_base(dnn_hip_session *s, const Wts &W, uint32_t woff, size_t pk, int ldw, int N, int K) {
     GemmArgs g{};
     g.W = W.w(woff);
     g.w_bytes = W.w_bytes(woff);
+    const size_t es = s->m->bf16 ? 2 : 4;
+    g.Wp = static_cast<const char *>(s->m->packed) + pk * es;
+    g.wp_bytes = (size_t)((N + 15) / 16) * 16 * (size_t)ldw * es;
     g.ldw = ldw;
     g.N = N;
     g.K = K;
@@ -195,7 +244,7 @@ int enqueue_layer(dnn_hip_session *s, int l, const PrefillPlan *pp) {
     const int M = pre ? pp->M : s->B;
     const bool bf = m->bf16 != 0;
 
-    GemmArgs g = gemm_base(s, W, lo.wqkv, ldD, 3 * D, ldD);
+    GemmArgs g = gemm_base(s, W, lo.wqkv, m->pk_l[(size_t)l * 4 + 0], ldD, 3 * D, ldD);
     g.A = e->X; g.lda = ldD; g.M = M;
     g.ks = pre ? 1 : pick_ks((3 * D + 15) / 16, ldD, M, true);
     g.part = e->part; g.cnt = e->cnt;
@@ -225,7 +274,7 @@ int enqueue_layer(dnn_hip_session *s, int l, const PrefillPlan *pp) {
         HIP_TRY(launch_attn(a, s->stream));
     }
 
-    g = gemm_base(s, W, lo.wo, ldD, D, ldD);
+    g = gemm_base(s, W, lo.wo, m->pk_l[(size_t)l * 4 + 1], ldD, D, ldD);
     g.A = e->ATT; g.lda = ldD; g.M = M;
     g.bias = W.f(lo.bo);
     g.out = e->X1; g.ldo = ldD; g.res = e->X; g.ldr = ldD;
@@ -234,7 +283,7 @@ int enqueue_layer(dnn_hip_session *s, int l, const PrefillPlan *pp) {
     g.part = e->part; g.cnt = e->cnt; g.kslot = 5 * l + 2;
     HIP_TRY(launch_gemm(EPI_RES, false, bf, pre, g, s->stream));
 
-    g = gemm_base(s, W, lo.wgu, ldD, 2 * m->F, ldD);
+    g = gemm_base(s, W, lo.wgu, m->pk_l[(size_t)l * 4 + 2], ldD, 2 * m->F, ldD);
     g.A = e->X1; g.lda = ldD; g.M = M;
     g.bias = W.f(lo.bg); g.bias2 = W.f(lo.bu);
     g.gamma = W.f(lo.g_ffn); g.eps = lo.eps_ffn; g.dnorm = D;
@@ -244,7 +293,7 @@ int enqueue_layer(dnn_hip_session *s, int l, const PrefillPlan *pp) {
     g.kslot = 5 * l + 3;
     HIP_TRY(launch_gemm(EPI_SWIGLU, true, bf, pre, g, s->stream));
 
-    g = gemm_base(s, W, lo.wd, ldF, D, ldF);
+    g = gemm_base(s, W, lo.wd, m->pk_l[(size_t)l * 4 + 3], ldF, D, ldF);
     g.A = e->ACT; g.lda = ldF; g.M = M;
     g.bias = W.f(lo.bd);
     g.out = e->X; g.ldo = ldD; g.res = e->X1; g.ldr = ldD;
@@ -262,7 +311,7 @@ int enqueue_head(dnn_hip_session *s, const PrefillPlan *pp, float *logits, int *
     const Wts W{m};
     const uint32_t embed = (uint32_t)(m->off.embed / 4), lm_bias = (uint32_t)(m->off.lm_bias / 4),
                    g_final = (uint32_t)(m->off.g_final / 4);
-    GemmArgs g = gemm_base(s, W, embed, m->ldD, m->V, m->ldD);
+    GemmArgs g = gemm_base(s, W, embed, m->pk_embed, m->ldD, m->V, m->ldD);
     g.A = e->X; g.lda = m->ldD; g.M = rows > 0 ? rows : s->B;
     g.arow = pp ? pp->arow : nullptr;
     g.bias = W.f(lm_bias);

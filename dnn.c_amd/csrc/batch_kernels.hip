@@ -111,6 +111,25 @@ __device__ __forceinline__ bool step_done(const StepState *st) {
 // rows first (L2), then its weights (HBM) -- before the first MFMA, so a
 // launch keeps its whole weight slice in flight at once.  KPW == 0 (prefill
 // shape): a loop over the k-steps, four per iteration.
+// DNNHIP_TRACE (timing builds only, never the product): thread 0 of each
+// workgroup stamps s_memrealtime at kernel phase boundaries during one chosen
+// decode step: trace[kernel slot][workgroup][event].
+#ifdef DNNHIP_TRACE
+constexpr int BT_SLOTS = 64, BT_WG = 1024, BT_EV = 8;
+__device__ unsigned long long g_btrace[BT_SLOTS * BT_WG * BT_EV];
+__device__ int g_btrace_step;
+#define BTRACE(ST, SLOT, EV)                                                                              \
+    do {                                                                                                  \
+        if (threadIdx.x == 0 && (ST)->t == g_btrace_step && (SLOT) < BT_SLOTS)                            \
+            g_btrace[((size_t)(SLOT) * BT_WG + (blockIdx.x + blockIdx.y * gridDim.x) % BT_WG) * BT_EV + (EV)] = \
+                __builtin_amdgcn_s_memrealtime();                                                         \
+    } while (0)
+#else
+#define BTRACE(ST, SLOT, EV) \
+    do {                     \
+    } while (0)
+#endif
+
 template <int MT, int NT, int WM, int WN, int KW, int KPW, bool BF, int EPI, bool NORM, bool AROW = false>
 __global__ __launch_bounds__(NTHR) void gemm_kernel(const GemmArgs g) {
     static_assert(WM * WN * KW == 4, "four wavefronts");
@@ -132,6 +151,7 @@ __global__ __launch_bounds__(NTHR) void gemm_kernel(const GemmArgs g) {
         done_flag = __builtin_nontemporal_load(&g.st->done);
     }
     const int tid = threadIdx.x, lane = tid & 63;
+    BTRACE(g.st, g.kslot, 0);
     const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int kw = w % KW, wn = (w / KW) % WN, wm = w / (KW * WN);
     const int tile_n = blockIdx.x / g.ks, ksi = blockIdx.x - tile_n * g.ks, tile_m = blockIdx.y;
@@ -219,10 +239,19 @@ __global__ __launch_bounds__(NTHR) void gemm_kernel(const GemmArgs g) {
             for (int mt = 0; mt < MT; mt++) a[u][mt] = lda4(ra, aoff[mt] + (unsigned)((kb0 + u) * 64));
             if (NORM) gm[u] = lda4(rg, (unsigned)(((kb0 + u) * 16 + 4 * q4) * 4));
         }
+        // weights from the fragment-ordered copy: one contiguous 1 KB (fp32)
+        // or 512 B (bf16) per wavefront load (row-major rows gave 16 separate
+        // 64-byte pieces per load, about 1 us slower per GEMM at 32 rows)
+        const rsrc_t rwp = buf(g.Wp, g.wp_bytes);
+        const int nkb = g.ldw / 16;
 #pragma unroll
         for (int u = 0; u < KPW; u++)
 #pragma unroll
-            for (int nt = 0; nt < NT; nt++) b[u][nt] = ldw4<BF>(rw, woff[nt] + (unsigned)((kb0 + u) * 16));
+            for (int nt = 0; nt < NT; nt++) {
+                const int t16 = tile_n * WN * NT + wn * NT + nt;
+                const unsigned po = (unsigned)(((size_t)t16 * nkb + kb0 + u) * 64 + lane) * 4u;
+                b[u][nt] = ldw4<BF>(rwp, po);
+            }
         // the RoPE loads wait for their positions: issue them only after every
         // main load is in flight (the empty asm keeps the compiler from
         // computing with the rows' positions before this point)
@@ -247,8 +276,13 @@ __global__ __launch_bounds__(NTHR) void gemm_kernel(const GemmArgs g) {
         // keep every load above the first MFMA (the scheduler would otherwise
         // sink loads towards their uses and serialise the HBM round trips)
         __builtin_amdgcn_sched_barrier(0);
+#ifdef DNNHIP_TRACE
+        __builtin_amdgcn_s_waitcnt(0);                  // timing builds: when every load has landed
+        BTRACE(g.st, g.kslot, 5);
+#endif
 #pragma unroll
         for (int u = 0; u < KPW; u++) kstep(a[u], b[u], gm[u]);
+        BTRACE(g.st, g.kslot, 1);
     } else {
         for (int kb = kb0; kb < kb1; kb += U) {
             f4 a[U][MT], b[U][NT], gm[U];
@@ -286,6 +320,7 @@ __global__ __launch_bounds__(NTHR) void gemm_kernel(const GemmArgs g) {
         }
     }
     __syncthreads();
+    BTRACE(g.st, g.kslot, 2);
     if (DEC && done_flag) return;
     const unsigned tag = s_tag * 128u + (unsigned)g.kslot;
 
@@ -314,6 +349,7 @@ __global__ __launch_bounds__(NTHR) void gemm_kernel(const GemmArgs g) {
                 put(rp, n_main + ((size_t)tile_n * g.ks + ksi) * g.M + gm_, sv, tag);
             }
         if (!arrive_last(g.cnt + tile_m * (gridDim.x / g.ks) + tile_n, (unsigned)g.ks, &s_flag)) return;
+        BTRACE(g.st, g.kslot, 3);
         if (NORM) {
             // the rows' sums of squares over all K, into ssl[0]
             for (int m = tid; m < BM; m += NTHR) {
@@ -441,6 +477,7 @@ __global__ __launch_bounds__(NTHR) void gemm_kernel(const GemmArgs g) {
             g.amax[(size_t)gm_ * ntn + tile_n] = make_uint2(as_uint(best), (unsigned)bi);
         }
     }
+    BTRACE(g.st, g.kslot, 4);
 }
 
 // The lm_head's argmax over its column tiles (gpt.c:220-230: the first index of
@@ -452,6 +489,7 @@ constexpr int FIN_ROWS = BK_MAXM / (FIN_THR / 64);     // rows per wavefront
 __global__ __launch_bounds__(FIN_THR) void head_finish_kernel(const GemmArgs g) {
     __shared__ int s_done[BK_MAXM];
     const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+    BTRACE(g.st, g.kslot + 1, 0);
     const int done = __builtin_nontemporal_load(&g.st->done);
     const int t = g.prefill ? 0 : g.st->t;
     const int ntn = g.amax_tiles;
@@ -538,6 +576,7 @@ __global__ __launch_bounds__(FIN_THR) void head_finish_kernel(const GemmArgs g) 
         if (!dr) s_all = 0;
     }
     __syncthreads();
+    BTRACE(g.st, g.kslot + 1, 1);
     if (tid == 0) {
         if (!g.prefill) {
             g.st->t = t + 1;
@@ -567,6 +606,7 @@ __global__ __launch_bounds__(64 * AW) void attn_kernel(const AttnArgs a) {
     const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int bh = blockIdx.x / a.nsplit, sp = blockIdx.x - bh * a.nsplit;
     const int m = bh / a.H, h = bh - m * a.H;
+    BTRACE(a.st, a.kslot, 0);
     if (tid == 0) s_tag = __builtin_nontemporal_load(&a.st->tag);
     const int r16 = lane & 15, q4 = lane >> 4;
     const size_t head = (((size_t)a.layer * a.B + m) * a.H + h) * (size_t)BK_DK * a.kv_s;
@@ -649,9 +689,11 @@ __global__ __launch_bounds__(64 * AW) void attn_kernel(const AttnArgs a) {
         o.x += __shfl_xor(o.x, o2); o.y += __shfl_xor(o.y, o2);
         o.z += __shfl_xor(o.z, o2); o.w += __shfl_xor(o.w, o2);
     }
+    BTRACE(a.st, a.kslot, 1);
     if (q4 == 0) *reinterpret_cast<f4 *>(&s_o[w][4 * r16]) = o;
     if (lane == 0) { s_ml[w][0] = mrun; s_ml[w][1] = lrun; }
     __syncthreads();
+    BTRACE(a.st, a.kslot, 2);
     // merge the wavefronts: thread d < 64 owns output dim d
     float om = -INFINITY;
     for (int k = 0; k < AW; k++) om = fmaxf(om, s_ml[k][0]);
@@ -948,6 +990,51 @@ hipError_t gemm_any(int epi, bool norm, bool prefill, const GemmArgs &g, hipStre
 }
 
 }  // namespace
+
+#ifdef DNNHIP_TRACE
+extern "C" int dnn_hip_btrace_arm(int step) {
+    static unsigned long long zero[BT_SLOTS * BT_WG * BT_EV];
+    if (hipMemcpyToSymbol(HIP_SYMBOL(g_btrace), zero, sizeof zero) != hipSuccess) return -1;
+    return hipMemcpyToSymbol(HIP_SYMBOL(g_btrace_step), &step, sizeof step) == hipSuccess ? 0 : -1;
+}
+extern "C" int dnn_hip_btrace_read(unsigned long long *out) {
+    return hipMemcpyFromSymbol(out, HIP_SYMBOL(g_btrace), sizeof(unsigned long long) * BT_SLOTS * BT_WG * BT_EV) ==
+                   hipSuccess ? 0 : -1;
+}
+#endif
+
+namespace {
+// One thread per (tile, k-block, lane): the lane's 4 elements of the fragment.
+template <bool BF>
+__global__ __launch_bounds__(256) void pack_kernel(const void *W, void *dst, int N, int ld, size_t total) {
+    const size_t i = (size_t)blockIdx.x * 256 + threadIdx.x;
+    if (i >= total) return;
+    const int nkb = ld / 16, lane = (int)(i & 63);
+    const size_t frag = i >> 6;
+    const int tile = (int)(frag / nkb), kb = (int)(frag - (size_t)tile * nkb);
+    const int row = tile * 16 + (lane & 15), col = kb * 16 + 4 * (lane >> 4);
+    if constexpr (BF) {
+        uint2 v = make_uint2(0u, 0u);
+        if (row < N) v = *reinterpret_cast<const uint2 *>(static_cast<const uint16_t *>(W) + (size_t)row * ld + col);
+        reinterpret_cast<uint2 *>(dst)[i] = v;
+    } else {
+        float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
+        if (row < N) v = *reinterpret_cast<const float4 *>(static_cast<const float *>(W) + (size_t)row * ld + col);
+        reinterpret_cast<float4 *>(dst)[i] = v;
+    }
+}
+}  // namespace
+
+hipError_t launch_pack(const void *W, void *dst, int N, int ld, bool bf16, hipStream_t stream) {
+    if (ld % 16) return hipErrorInvalidValue;
+    const size_t total = (size_t)((N + 15) / 16) * (ld / 16) * 64;
+    const unsigned blocks = (unsigned)((total + 255) / 256);
+    if (bf16)
+        hipLaunchKernelGGL(pack_kernel<true>, dim3(blocks), dim3(256), 0, stream, W, dst, N, ld, total);
+    else
+        hipLaunchKernelGGL(pack_kernel<false>, dim3(blocks), dim3(256), 0, stream, W, dst, N, ld, total);
+    return hipGetLastError();
+}
 
 hipError_t launch_gemm(int epi, bool norm, bool bf16, bool prefill, const GemmArgs &g, hipStream_t stream) {
     return bf16 ? gemm_any<true>(epi, norm, prefill, g, stream) : gemm_any<false>(epi, norm, prefill, g, stream);

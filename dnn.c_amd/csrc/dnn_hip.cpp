@@ -144,6 +144,7 @@ int upload(dnn_hip_model *m, const float *const *params, int n_params) {
     }
     HIP_TRY(hipSetDevice(m->device));
     HIP_TRY(hipMemcpy(m->arena, host.data(), m->arena_bytes, hipMemcpyHostToDevice));
+    m->packed_valid = false;                 // the batched engine repacks at its next use
     return DNN_HIP_OK;
 }
 
@@ -302,6 +303,7 @@ int dnn_hip_model_destroy(dnn_hip_model *m) {
     (void)hipSetDevice(m->device);
     if (m->arena) (void)hipFree(m->arena);
     if (m->arena16) (void)hipFree(m->arena16);
+    if (m->packed) (void)hipFree(m->packed);
     if (m->d_layers) (void)hipFree(m->d_layers);
     if (m->rope) (void)hipFree(m->rope);
     delete m;

@@ -26,6 +26,15 @@ struct dnn_hip_model {
     int rope_rows = 0;
     // byte offsets of every device tensor inside the arena, for the uploads
     struct Off { size_t embed, lm_bias, g_final; std::vector<size_t> l; } off;
+    // the weight matrices again in MFMA fragment order for the batched decode
+    // GEMMs (built on the device at first use, rebuilt after an update):
+    // matrix of N rows and ld columns -> [ceil(N/16)][ld/16][64 lanes][4],
+    // lane l holding row 16t + l%16, columns 16kb + 4(l/16) .. +3
+    void *packed = nullptr;
+    size_t packed_bytes = 0;
+    bool packed_valid = false;
+    size_t pk_embed = 0;             // element offsets in `packed`
+    std::vector<size_t> pk_l;        // [L][4]: wqkv, wo, wgu, wd
 };
 
 // Buffers of the batched engine (one per session that uses it).
