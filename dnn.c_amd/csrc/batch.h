@@ -52,6 +52,8 @@ struct GemmArgs {
     size_t w_bytes;             // bytes from W to the end of its arena (loads past it read 0)
     const void *Wp;             // the same matrix in fragment order (decode shape), or null
     size_t wp_bytes;            // bytes of the packed matrix
+    int pk;                     // 1 (decode steps): A, the residual, the RES / SWIGLU outputs and the
+                                // next step's embedding rows are in fragment order (pk_index)
     int ldw, N, K;
     int ks;                     // workgroups per column tile (split K), >= 1
     int mt_max;                 // decode shape: at most this many 16-row tiles per workgroup (0: all rows)
@@ -106,6 +108,7 @@ struct AttnArgs {
     unsigned *cnt;              // [M*H]
     StepState *st;
     int kslot;
+    int pk;                     // att rows in fragment order (pk_index)
 };
 
 // Prefill attention over the new rows of each sequence: logical rows
@@ -130,12 +133,21 @@ struct EmbedArgs {
     const int *ids;
     float *out;
     int M, ld, D;
+    int pk;                     // out in fragment order (pk_index)
     StepState *st;              // non-null: reset the step counters of a decode call
     int *row_done;              // non-null: cleared
 };
 
 // host-side launchers (batch_kernels.hip); all enqueue on `stream` and return
 // a hipError_t.  bf16: W holds bf16 weights.
+// Element (m, k) of an activation buffer of row length ld (a multiple of 16)
+// in MFMA fragment order: [m/16][k/16][lane = m%16 + 16*((k%16)/4)][k%4], so a
+// wavefront's A operand for 16 rows x 16 columns is one contiguous 1 KB piece.
+__host__ __device__ inline size_t pk_index(int m, int k, int ld) {
+    return ((((size_t)(m >> 4) * (size_t)(ld >> 4) + (size_t)(k >> 4)) << 6) + (size_t)((m & 15) + ((k & 15) >> 2) * 16)) * 4 +
+           (size_t)(k & 3);
+}
+
 // W (N rows of ld elements, fp32 or bf16) -> dst in fragment order
 // [ceil(N/16)][ld/16][64][4], rows past N zero.
 hipError_t launch_pack(const void *W, void *dst, int N, int ld, bool bf16, hipStream_t stream);

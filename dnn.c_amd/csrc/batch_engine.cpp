@@ -127,7 +127,23 @@ int ensure_packed(dnn_hip_model *m, hipStream_t stream) {
     return DNN_HIP_OK;
 }
 
-int engine_get(dnn_hip_session *s, int rows) {
+// The activation buffers' layout for the next launches: decode steps keep X,
+// X1, ATT and ACT in fragment order, every other path row-major.  A change
+// clears them, so the padding columns past d_model / d_ffn (summed into the
+// folded rms_norm, met by zero weights) are zero in the new layout too.
+int set_layout(dnn_hip_session *s, int layout) {
+    BatchEngine *e = s->eng;
+    if (e->layout == layout) return DNN_HIP_OK;
+    const size_t ldD = s->m->ldD, ldF = s->m->ldF, mc = (size_t)e->mcap;
+    HIP_TRY(hipMemsetAsync(e->X, 0, mc * ldD * 4, s->stream));
+    HIP_TRY(hipMemsetAsync(e->X1, 0, mc * ldD * 4, s->stream));
+    HIP_TRY(hipMemsetAsync(e->ATT, 0, mc * ldD * 4, s->stream));
+    HIP_TRY(hipMemsetAsync(e->ACT, 0, mc * ldF * 4, s->stream));
+    e->layout = layout;
+    return DNN_HIP_OK;
+}
+
+int engine_get(dnn_hip_session *s, int rows, int layout = 0) {
     dnn_hip_model *m = s->m;
     {
         const int rc = ensure_packed(m, s->stream);
@@ -192,8 +208,9 @@ int engine_get(dnn_hip_session *s, int rows) {
         HIP_TRY(hipMemset(e->Q, 0, mc * (size_t)m->D * 4));
         HIP_TRY(hipMemset(e->ACT, 0, mc * ldF * 4));
         e->mcap = mc;
+        e->layout = 0;
     }
-    return DNN_HIP_OK;
+    return set_layout(s, layout);
 }
 
 struct Wts {
@@ -256,6 +273,7 @@ int enqueue_layer(dnn_hip_session *s, int l, const PrefillPlan *pp) {
     g.H = m->H; g.kv_s = s->kv_s; g.B = s->B; g.layer = l;
     g.rope = m->rope; g.rope_rows = m->rope_rows;
     g.kslot = 5 * l;
+    g.pk = !pre;
     HIP_TRY(launch_gemm(EPI_QKV, true, bf, pre, g, s->stream));
 
     if (pre) {
@@ -271,6 +289,7 @@ int enqueue_layer(dnn_hip_session *s, int l, const PrefillPlan *pp) {
         a.M = M; a.H = m->H; a.kv_s = s->kv_s; a.layer = l; a.D = D; a.B = s->B; a.ldatt = ldD;
         a.nsplit = attn_splits(M, m->H);
         a.part = e->apart; a.cnt = e->cnt + CNT_GEMM; a.st = e->st; a.kslot = 5 * l + 1;
+        a.pk = 1;                               // decode steps: ATT in fragment order
         HIP_TRY(launch_attn(a, s->stream));
     }
 
@@ -281,6 +300,7 @@ int enqueue_layer(dnn_hip_session *s, int l, const PrefillPlan *pp) {
     g.mt_max = 1;          // out_proj: one 16-row tile per workgroup (more, lighter workgroups)
     g.ks = pre ? 1 : pick_ks((D + 15) / 16, ldD, M, false, g.mt_max);
     g.part = e->part; g.cnt = e->cnt; g.kslot = 5 * l + 2;
+    g.pk = !pre;
     HIP_TRY(launch_gemm(EPI_RES, false, bf, pre, g, s->stream));
 
     g = gemm_base(s, W, lo.wgu, m->pk_l[(size_t)l * 4 + 2], ldD, 2 * m->F, ldD);
@@ -291,6 +311,7 @@ int enqueue_layer(dnn_hip_session *s, int l, const PrefillPlan *pp) {
     g.ks = pre ? 1 : pick_ks((2 * m->F + 15) / 16, ldD, M, true);
     g.part = e->part; g.cnt = e->cnt;
     g.kslot = 5 * l + 3;
+    g.pk = !pre;
     HIP_TRY(launch_gemm(EPI_SWIGLU, true, bf, pre, g, s->stream));
 
     g = gemm_base(s, W, lo.wd, m->pk_l[(size_t)l * 4 + 3], ldF, D, ldF);
@@ -299,6 +320,7 @@ int enqueue_layer(dnn_hip_session *s, int l, const PrefillPlan *pp) {
     g.out = e->X; g.ldo = ldD; g.res = e->X1; g.ldr = ldD;
     g.ks = pre ? 1 : pick_ks((D + 15) / 16, ldF, M, false);
     g.part = e->part; g.cnt = e->cnt; g.kslot = 5 * l + 4;
+    g.pk = !pre;
     HIP_TRY(launch_gemm(EPI_RES, false, bf, pre, g, s->stream));
     return DNN_HIP_OK;
 }
@@ -322,6 +344,7 @@ int enqueue_head(dnn_hip_session *s, const PrefillPlan *pp, float *logits, int *
     g.x_next = e->X; g.ldx = m->ldD; g.embed = W.f(embed);
     g.steps_done = e->steps_done; g.eos = eos; g.row_done = e->row_done;
     g.prefill = pp != nullptr;
+    g.pk = pp == nullptr;                    // decode steps: X in fragment order
     g.kslot = 5 * m->L;
     g.ks = pick_ks((m->V + 15) / 16, m->ldD, g.M, true);
     g.amax_tiles = (m->V + 15) / 16;
@@ -355,7 +378,7 @@ int engine_decode(dnn_hip_session *s, const int *feed, int n_feed_all, const int
     int rc = check_decode(s, feed, n_feed_all, n_feed, n_steps, nf, &nf_max);
     if (rc) return rc;
     HIP_TRY(hipSetDevice(m->device));
-    rc = engine_get(s, round_up(B, 16));
+    rc = engine_get(s, round_up(B, 16), 1);
     if (!rc) rc = grow(&s->feed, &s->feed_cap, (size_t)nf_max * B);
     if (!rc) rc = grow(&s->ids, &s->ids_cap, (size_t)n_steps * B);
     if (!rc && logits) rc = grow(&s->logits, &s->logits_cap, (size_t)n_steps * B * m->V);
@@ -387,6 +410,7 @@ int engine_decode(dnn_hip_session *s, const int *feed, int n_feed_all, const int
     EmbedArgs ea{};
     ea.embed = reinterpret_cast<const float *>(m->arena) + m->off.embed / 4;
     ea.ids = s->feed; ea.out = e->X; ea.M = B; ea.ld = m->ldD; ea.D = m->D; ea.st = e->st; ea.row_done = e->row_done;
+    ea.pk = 1;                               // decode steps keep X in fragment order
     HIP_TRY(launch_embed(ea, s->stream));
     HIP_TRY(hipEventRecord(s->ev0, s->stream));
     for (int t = 0; t < n_steps; t++) HIP_TRY(hipGraphLaunch(e->gexec, s->stream));

@@ -173,8 +173,11 @@ __global__ __launch_bounds__(NTHR) void gemm_kernel(const GemmArgs g) {
         // a row map only where one is used (a possible load here would make
         // every later wait cover it)
         if (AROW) pm = g.arow[m < g.M ? m : 0];
-        aoff[mt] = (unsigned)(((size_t)pm * g.lda + 4 * q4) * 4);
+        aoff[mt] = g.pk ? (unsigned)((((size_t)(tile_m * (BM / 16) + wm * MT + mt) * (g.lda / 16)) * 64 + lane) * 16)
+                        : (unsigned)(((size_t)pm * g.lda + 4 * q4) * 4);
     }
+    // bytes between consecutive 16-column k-blocks of A
+    const unsigned astep = g.pk ? 1024u : 64u;
 #pragma unroll
     for (int nt = 0; nt < NT; nt++) {
         const int n = tile_n * BN + wn * 16 * NT + 16 * nt + r16;
@@ -226,7 +229,11 @@ __global__ __launch_bounds__(NTHR) void gemm_kernel(const GemmArgs g) {
             if (i >= BM * BN / 2 || gm_ >= g.M || gn >= g.N) continue;
             if (EPI == EPI_SWIGLU) { eb0[e] = g.bias[gn >> 1]; eb1[e] = g.bias2[gn >> 1]; }
             else { eb0[e] = g.bias[gn]; eb1[e] = g.bias[gn + 1]; }
-            if (EPI == EPI_RES) { er0[e] = g.res[(size_t)gm_ * g.ldr + gn]; er1[e] = g.res[(size_t)gm_ * g.ldr + gn + 1]; }
+            if (EPI == EPI_RES) {
+                const size_t ri = g.pk ? pk_index(gm_, gn, g.ldr) : (size_t)gm_ * g.ldr + gn;   // gn even: gn+1 follows
+                er0[e] = g.res[ri];
+                er1[e] = g.res[ri + 1];
+            }
             if (EPI == EPI_QKV) { erb[e] = g.row_b[gm_]; erp[e] = g.row_p[gm_]; }
         }
     }
@@ -236,7 +243,7 @@ __global__ __launch_bounds__(NTHR) void gemm_kernel(const GemmArgs g) {
 #pragma unroll
         for (int u = 0; u < KPW; u++) {
 #pragma unroll
-            for (int mt = 0; mt < MT; mt++) a[u][mt] = lda4(ra, aoff[mt] + (unsigned)((kb0 + u) * 64));
+            for (int mt = 0; mt < MT; mt++) a[u][mt] = lda4(ra, aoff[mt] + (unsigned)(kb0 + u) * astep);
             if (NORM) gm[u] = lda4(rg, (unsigned)(((kb0 + u) * 16 + 4 * q4) * 4));
         }
         // weights from the fragment-ordered copy: one contiguous 1 KB (fp32)
@@ -417,16 +424,17 @@ __global__ __launch_bounds__(NTHR) void gemm_kernel(const GemmArgs g) {
         const int ei = DEC ? e : 0;
         if (EPI == EPI_RES) {
             const float y0 = v0 + (pf ? eb0[ei] : g.bias[gn]), y1 = v1 + (pf ? eb1[ei] : g.bias[gn + 1]);
-            const float r0 = pf ? er0[ei] : g.res[(size_t)gm_ * g.ldr + gn];
-            const float r1 = pf ? er1[ei] : g.res[(size_t)gm_ * g.ldr + gn + 1];
-            float *o = g.out + (size_t)gm_ * g.ldo + gn;
+            const size_t ri = g.pk ? pk_index(gm_, gn, g.ldr) : (size_t)gm_ * g.ldr + gn;
+            const float r0 = pf ? er0[ei] : g.res[ri];
+            const float r1 = pf ? er1[ei] : g.res[ri + 1];
+            float *o = g.out + (g.pk ? pk_index(gm_, gn, g.ldo) : (size_t)gm_ * g.ldo + gn);
             o[0] = r0 + y0;
             o[1] = r1 + y1;
         } else if (EPI == EPI_SWIGLU) {
             // rows 2f (gate) and 2f+1 (up) of the interleaved gate/up matrix
             const int f = gn >> 1;
             const float gt = v0 + (pf ? eb0[ei] : g.bias[f]), up = v1 + (pf ? eb1[ei] : g.bias2[f]);
-            g.out[(size_t)gm_ * g.ldo + f] = (gt / (1.0f + expf(-gt))) * up;
+            g.out[g.pk ? pk_index(gm_, f, g.ldo) : (size_t)gm_ * g.ldo + f] = (gt / (1.0f + expf(-gt))) * up;
         } else if (EPI == EPI_QKV) {
             float y0 = v0 + (pf ? eb0[ei] : g.bias[gn]), y1 = v1 + (pf ? eb1[ei] : g.bias[gn + 1]);
             const int sec = gn / g.D, c = gn - sec * g.D, h = c / BK_DK, d = c - h * BK_DK;
@@ -556,14 +564,15 @@ __global__ __launch_bounds__(FIN_THR) void head_finish_kernel(const GemmArgs g) 
         // would otherwise serialise the copy)
         const int nxt = (t + 1 < nf[r]) ? g.feed[(size_t)(t + 1) * g.M + m] : tok;
         const float *e = g.embed + (size_t)nxt * g.ldx;
-        float *x = g.x_next + (size_t)m * g.ldx;
         constexpr int CPL = BK_MAXD / 64;
         float ev[CPL];
 #pragma unroll
         for (int j = 0; j < CPL; j++) ev[j] = (lane + 64 * j < g.D) ? e[lane + 64 * j] : 0.f;
 #pragma unroll
-        for (int j = 0; j < CPL; j++)
-            if (lane + 64 * j < g.D) x[lane + 64 * j] = ev[j];
+        for (int j = 0; j < CPL; j++) {
+            const int c = lane + 64 * j;
+            if (c < g.D) g.x_next[g.pk ? pk_index(m, c, g.ldx) : (size_t)m * g.ldx + c] = ev[j];
+        }
     }
     __syncthreads();
     // rows that stopped in an earlier step stay stopped; one thread per row
@@ -707,7 +716,10 @@ __global__ __launch_bounds__(64 * AW) void attn_kernel(const AttnArgs a) {
         }
     }
     if (a.nsplit == 1) {
-        if (tid < BK_DK) a.att[(size_t)m * a.ldatt + h * BK_DK + tid] = od / ol;
+        if (tid < BK_DK) {
+            const int c = h * BK_DK + tid;
+            a.att[a.pk ? pk_index(m, c, a.ldatt) : (size_t)m * a.ldatt + c] = od / ol;
+        }
         return;
     }
     // publish (o, m, l) of this split as tagged pairs; the last split of the
@@ -756,7 +768,8 @@ __global__ __launch_bounds__(64 * AW) void attn_kernel(const AttnArgs a) {
         gl += as_float(pl[k].x) * f;
         gd += as_float(po[k].x) * f;
     }
-    a.att[(size_t)m * a.ldatt + h * BK_DK + tid] = gd / gl;
+    const int c = h * BK_DK + tid;
+    a.att[a.pk ? pk_index(m, c, a.ldatt) : (size_t)m * a.ldatt + c] = gd / gl;
 }
 
 // ---------------------------------------------------------------------------
@@ -898,8 +911,7 @@ __global__ __launch_bounds__(NTHR) void embed_kernel(const EmbedArgs a) {
     const int id = a.ids[m];
     if (id < 0) return;
     const float *e = a.embed + (size_t)id * a.ld;
-    float *x = a.out + (size_t)m * a.ld;
-    for (int c = threadIdx.x; c < a.D; c += NTHR) x[c] = e[c];
+    for (int c = threadIdx.x; c < a.D; c += NTHR) a.out[a.pk ? pk_index(m, c, a.ld) : (size_t)m * a.ld + c] = e[c];
 }
 
 // ---------------------------------------------------------------------------

@@ -40,6 +40,7 @@ struct dnn_hip_model {
 // Buffers of the batched engine (one per session that uses it).
 struct BatchEngine {
     int mcap = 0;                    // rows the activation buffers hold
+    int layout = 0;                  // of X, X1, ATT, ACT: 0 row-major (prefill, layer calls), 1 fragment order (decode)
     float *X = nullptr, *X1 = nullptr, *ATT = nullptr, *Q = nullptr, *ACT = nullptr;
     uint2 *part = nullptr;           // split-K partials of the decode GEMMs
     size_t part_pairs = 0;
