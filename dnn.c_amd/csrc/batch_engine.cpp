@@ -290,6 +290,7 @@ int enqueue_layer(dnn_hip_session *s, int l, const PrefillPlan *pp) {
         a.nsplit = attn_splits(M, m->H);
         a.part = e->apart; a.cnt = e->cnt + CNT_GEMM; a.st = e->st; a.kslot = 5 * l + 1;
         a.pk = 1;                               // decode steps: ATT in fragment order
+        a.spec = e->att_spec;
         HIP_TRY(launch_attn(a, s->stream));
     }
 
@@ -387,10 +388,29 @@ int engine_decode(dnn_hip_session *s, const int *feed, int n_feed_all, const int
     HIP_TRY(hipMemcpyAsync(s->feed, feed, sizeof(int) * (size_t)nf_max * B, hipMemcpyHostToDevice, s->stream));
     HIP_TRY(hipMemcpyAsync(s->n_feed, nf.data(), sizeof(int) * B, hipMemcpyHostToDevice, s->stream));
 
-    // the step graph, captured again when a buffer it names changed
+    // the decode attention's speculative loads: the leading wavefronts whose
+    // first chunk (64 keys of split 0) at least 3/4 of this call's (row, step)
+    // pairs have, at least one
+    {
+        const int ns = attn_splits(B, m->H);
+        int spec = 1;
+        for (int w = 1; w < 4; w++) {
+            const long long keys = 64LL * ns * w;
+            long long have = 0;
+            for (int b = 0; b < B; b++) {
+                const long long first = keys - s->h_pos[b];      // steps t with h_pos + t + 1 > keys: t >= first
+                have += std::max(0LL, (long long)n_steps - std::max(0LL, first));
+            }
+            if (4 * have < 3LL * B * n_steps) break;
+            spec = w + 1;
+        }
+        e->att_spec = spec;
+    }
+    // the step graph, captured again when a buffer it names or a launch
+    // parameter changed
     float *lg = logits ? s->logits : nullptr;
     const void *key[4] = {s->feed, s->ids, lg, e->X};
-    if (!e->gexec || e->geos != eos || memcmp(key, e->gkey, sizeof key) != 0) {
+    if (!e->gexec || e->geos != eos || e->gspec != e->att_spec || memcmp(key, e->gkey, sizeof key) != 0) {
         drop_graph(e);
         HIP_TRY(hipStreamBeginCapture(s->stream, hipStreamCaptureModeThreadLocal));
         int erc = 0;
@@ -405,6 +425,7 @@ int engine_decode(dnn_hip_session *s, const int *feed, int n_feed_all, const int
         if (ie != hipSuccess) { e->gexec = nullptr; return set_error(DNN_HIP_EDEVICE, "step graph: %s", hipGetErrorString(ie)); }
         memcpy(e->gkey, key, sizeof key);
         e->geos = eos;
+        e->gspec = e->att_spec;
     }
     // the first step's embedding rows; resets the step counter, done flags
     EmbedArgs ea{};

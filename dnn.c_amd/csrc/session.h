@@ -61,6 +61,8 @@ struct BatchEngine {
     // the captured decode step
     hipGraphExec_t gexec = nullptr;
     const void *gkey[4] = {nullptr, nullptr, nullptr, nullptr};
+    int att_spec = 4;                // decode attention: wavefronts that load before the row length is known
+    int gspec = -1;                  // att_spec of the captured step graph
     int geos = -2;
 };
 
