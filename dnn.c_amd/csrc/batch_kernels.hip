@@ -495,14 +495,17 @@ __global__ __launch_bounds__(NTHR) void gemm_kernel(const GemmArgs g) {
 constexpr int FIN_THR = 1024;
 constexpr int FIN_ROWS = BK_MAXM / (FIN_THR / 64);     // rows per wavefront
 __global__ __launch_bounds__(FIN_THR) void head_finish_kernel(const GemmArgs g) {
-    __shared__ int s_done[BK_MAXM];
+    __shared__ int s_all;
     const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
     BTRACE(g.st, g.kslot + 1, 0);
     const int done = __builtin_nontemporal_load(&g.st->done);
     const int t = g.prefill ? 0 : g.st->t;
     const int ntn = g.amax_tiles;
-    if (tid < BK_MAXM) s_done[tid] = 0;
-    int nf[FIN_ROWS];
+    if (tid == 0) s_all = g.eos >= 0;
+    // every row's inputs that do not depend on this step's token, loaded up
+    // front: prompt length, position, stop flag, and (once the step is known)
+    // the next prompt id
+    int nf[FIN_ROWS], ps[FIN_ROWS], rd[FIN_ROWS], fnext[FIN_ROWS];
     float best[FIN_ROWS];
     int bi[FIN_ROWS];
 #pragma unroll
@@ -510,7 +513,15 @@ __global__ __launch_bounds__(FIN_THR) void head_finish_kernel(const GemmArgs g) 
         best[r] = -INFINITY;
         bi[r] = 0x7fffffff;
         const int m = w + 16 * r;
-        nf[r] = (!g.prefill && m < g.M) ? g.n_feed[m] : 0;
+        const bool row = !g.prefill && m < g.M;
+        nf[r] = row ? g.n_feed[m] : 0;
+        ps[r] = row ? g.pos[m] : 0;
+        rd[r] = row ? g.row_done[m] : 0;
+    }
+#pragma unroll
+    for (int r = 0; r < FIN_ROWS; r++) {
+        const int m = w + 16 * r;
+        fnext[r] = (!g.prefill && m < g.M && t + 1 < nf[r]) ? g.feed[(size_t)(t + 1) * g.M + m] : -1;
     }
     // the partials in passes of FIN_PASS tiles per lane, every load of a pass
     // (all rows of the wavefront) issued before the first compare; tiles in
@@ -535,7 +546,7 @@ __global__ __launch_bounds__(FIN_THR) void head_finish_kernel(const GemmArgs g) 
             }
     }
     if (done) return;
-    __syncthreads();
+    __syncthreads();                                   // s_all initialised
 #pragma unroll
     for (int r = 0; r < FIN_ROWS; r++) {
         const int m = w + 16 * r;
@@ -556,13 +567,16 @@ __global__ __launch_bounds__(FIN_THR) void head_finish_kernel(const GemmArgs g) 
         const bool greedy = t >= nf[r] - 1;
         if (lane == 0) {
             g.ids[(size_t)t * g.M + m] = tok;
-            s_done[m] = g.eos >= 0 && greedy && tok == g.eos;
-            g.pos[m] += 1;
+            g.pos[m] = ps[r] + 1;
+            // rows that stopped in an earlier step stay stopped
+            const int dr = rd[r] | (g.eos >= 0 && greedy && tok == g.eos);
+            g.row_done[m] = dr;
+            if (!dr) atomicAnd(&s_all, 0);
         }
         // the next step's embedding row (embedding.c:79-84): every load of the
         // row before the first store (a store may alias a later load, which
         // would otherwise serialise the copy)
-        const int nxt = (t + 1 < nf[r]) ? g.feed[(size_t)(t + 1) * g.M + m] : tok;
+        const int nxt = fnext[r] >= 0 ? fnext[r] : tok;
         const float *e = g.embed + (size_t)nxt * g.ldx;
         constexpr int CPL = BK_MAXD / 64;
         float ev[CPL];
@@ -573,16 +587,6 @@ __global__ __launch_bounds__(FIN_THR) void head_finish_kernel(const GemmArgs g) 
             const int c = lane + 64 * j;
             if (c < g.D) g.x_next[g.pk ? pk_index(m, c, g.ldx) : (size_t)m * g.ldx + c] = ev[j];
         }
-    }
-    __syncthreads();
-    // rows that stopped in an earlier step stay stopped; one thread per row
-    __shared__ int s_all;
-    if (tid == 0) s_all = g.eos >= 0;
-    __syncthreads();
-    if (!g.prefill && tid < g.M) {
-        const int dr = s_done[tid] | g.row_done[tid];
-        g.row_done[tid] = dr;
-        if (!dr) s_all = 0;
     }
     __syncthreads();
     BTRACE(g.st, g.kslot + 1, 1);
