@@ -25,6 +25,7 @@ HIP_SYMBOLS = [
     "dnn_hip_decode", "dnn_hip_generate", "dnn_hip_session_last_ms", "dnn_hip_session_set_grid",
     "dnn_hip_session_grid", "dnn_hip_session_kernel", "dnn_hip_session_att_splits", "dnn_hip_model_create_ex", "dnn_hip_prefill",
     "dnn_hip_block_forward", "dnn_hip_head_forward", "dnn_hip_embed", "dnn_hip_cache_read", "dnn_hip_rms_norm",
+    "dnn_hip_linear",
 ]
 
 WEIGHTS_F32 = 0

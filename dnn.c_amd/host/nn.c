@@ -2,6 +2,8 @@
  * 40-59, 152-167, 177-191).  Creation order and bounds are the reference's, so
  * the same dnn_seed() yields the same weights. */
 #include "dnn/nn.h"
+#include "dnn_hip.h"
+#include "device.h"
 #include <assert.h>
 #include <math.h>
 #include <string.h>
@@ -18,6 +20,40 @@ linear *linear_create(struct mem_pool *params, int in_features, int out_features
     module_param(&l->base, "weight", l->weight);
     module_param(&l->base, "bias", l->bias);
     return l;
+}
+
+conv2d *conv2d_create(struct mem_pool *params, int in_channels, int out_channels, int kernel_size, int stride,
+                      int padding) {
+    assert(in_channels > 0 && out_channels > 0 && kernel_size > 0);
+    conv2d *c = _mem_pool_alloc(params, sizeof(conv2d), NULL);
+    module_init(&c->base, params, "conv2d");
+    c->in_channels = in_channels;
+    c->out_channels = out_channels;
+    c->kernel_size = kernel_size;
+    c->stride = stride;
+    c->padding = padding;
+    const float bound = sqrtf(6.0f / (float)(in_channels * kernel_size * kernel_size));
+    c->weight = tensor_uniform(params, 4, (int[]){out_channels, in_channels, kernel_size, kernel_size}, 1, bound);
+    c->bias = tensor_zeros(params, 1, (int[]){out_channels}, 1);
+    module_param(&c->base, "weight", c->weight);
+    module_param(&c->base, "bias", c->bias);
+    return c;
+}
+
+tensor *linear_forward(struct mem_pool *scratch, linear *l, const tensor *input) {
+    assert(l && input);
+    assert(input->ndim >= 2 && "linear_forward: input must be at least 2D");
+    assert(input->shape[input->ndim - 1] == l->in_features && "linear_forward: last dim of input must match in_features");
+    assert(input->contiguous && "linear_forward: contiguous input");
+    const int n = tensor_numel(input) / l->in_features;
+    int shape[DNN_MAX_DIMS];
+    for (int i = 0; i < input->ndim; i++) shape[i] = input->shape[i];
+    shape[input->ndim - 1] = l->out_features;
+    tensor *y = tensor_scratch(scratch, input->ndim, shape, 0);
+    dnn_amd_check(dnn_hip_linear((const float *)input->data + input->offset, n, l->in_features, tensor_data_ptr(l->weight), 0,
+                                 tensor_data_ptr(l->bias), l->out_features, tensor_data_ptr(y)),
+                  "dnn_hip_linear");
+    return y;
 }
 
 swiglu_ffn *swiglu_ffn_create(struct mem_pool *params, int d_model, int intermediate_size) {

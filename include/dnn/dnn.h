@@ -13,4 +13,5 @@
 #include "tokenizer.h"
 #include "transformer.h"
 #include "gpt.h"
+#include "vlm.h"
 #endif

@@ -36,7 +36,27 @@ typedef struct embedding {
     int     d_model;
 } embedding;
 
+/* conv2d (reference nn.h:107-116): weight [out][in][k][k], bias [out].  Here
+ * only as vision_lm's patch embedding (kernel = stride = patch, no padding). */
+typedef struct conv2d {
+    module  base;
+    tensor *weight;
+    tensor *bias;
+    int     in_channels;
+    int     out_channels;
+    int     kernel_size;
+    int     stride;
+    int     padding;
+} conv2d;
+
 linear     *linear_create(struct mem_pool *params, int in_features, int out_features);
+/* conv2d_create (nn.c:90-110): weight ~ U(-b, b), b = sqrt(6 / (in * k * k)),
+ * bias 0 -- the same draws from the default stream as the reference. */
+conv2d     *conv2d_create(struct mem_pool *params, int in_channels, int out_channels, int kernel_size, int stride,
+                          int padding);
+/* linear_forward (nn.c:27-36): x [..., in] -> x . W + b [..., out], on the
+ * device (dnn_hip_linear). */
+tensor     *linear_forward(struct mem_pool *scratch, linear *l, const tensor *input);
 swiglu_ffn *swiglu_ffn_create(struct mem_pool *params, int d_model, int intermediate_size);
 rms_norm   *rms_norm_create(struct mem_pool *params, int d, float eps);
 embedding  *embedding_create(struct mem_pool *params, int vocab_size, int d_model);

@@ -171,6 +171,14 @@ int dnn_hip_rms_norm(dnn_hip_session *s, const float *x, const float *gamma, int
  * (kv_cache_get_K / kv_cache_get_V, transformer.c:90-112). */
 int dnn_hip_cache_read(dnn_hip_session *s, int layer, int which, int len, float *out);
 
+/* y [n][out] = x [n][in] . W + b on the device -- linear_forward (nn.c:27-36,
+ * tensor_matmul_add) for weights the caller holds: w_layout 0 = W [in][out]
+ * (the reference's linear), 1 = W [out][in] (a conv2d weight [out][C][k][k]
+ * flattened, as vision_lm's patch embedding uses it, vlm.c:175-186).  b may be
+ * NULL.  x, W, b, y are host memory; synchronous. */
+int dnn_hip_linear(const float *x, int n, int in, const float *w, int w_layout, const float *b, int out,
+                   float *y);
+
 /* decoder_lm_generate(use_cache=1, temperature=0) for one sequence: out gets
  * prompt + generated ids (P + max_new ints), *n_out its length (stops after eos
  * when eos >= 0).  Uses a fresh session of max_seq = P + max_new. */

@@ -44,3 +44,14 @@ def generate_main(built, tmp_path_factory):
                            os.path.join(ROOT, "tests", "c", "generate_main.c"), "-o", exe,
                            "-L" + libdir, "-ldnn_amd", "-Wl,-rpath," + libdir, "-lm"])
     return exe
+
+
+@pytest.fixture(scope="session")
+def vlm_main(built, tmp_path_factory):
+    """tests/c/vlm_main.c (a vision_lm caller) built against include/dnn + libdnn_amd.so."""
+    exe = str(tmp_path_factory.mktemp("c") / "vlm_main")
+    libdir = os.path.join(ROOT, "dnn.c_amd", "lib")
+    subprocess.check_call(["gcc", "-std=gnu11", "-O2", "-Wall", "-I" + os.path.join(ROOT, "include"),
+                           os.path.join(ROOT, "tests", "c", "vlm_main.c"), "-o", exe,
+                           "-L" + libdir, "-ldnn_amd", "-Wl,-rpath," + libdir, "-lm"])
+    return exe

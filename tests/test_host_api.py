@@ -8,6 +8,8 @@ import subprocess
 import numpy as np
 import pytest
 
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+
 
 def run(exe, *args):
     out = subprocess.check_output([exe] + [str(a) for a in args], text=True, timeout=300)
@@ -33,3 +35,14 @@ def test_c_api_builds_reference_weights_c2(generate_main, golden):
 def test_c_api_create_only_weights(generate_main, golden):
     r = run(generate_main, 128, 256, 4, 4, 683, 256, 7, "create", 1, 4, 0)
     assert r["params"] == golden["c1_create_params"]
+
+
+def test_vision_lm_weights_match_reference(vlm_main):
+    """vision_lm_create + vision_lm_init_weights + enable_rope through the
+    reference's API give the reference's parameters bit for bit (patch conv,
+    img_proj, the decoder, image positions; vlm.c:20-127)."""
+    with open(os.path.join(ROOT, "tests", "golden", "data", "vlm_gen.json")) as f:
+        g = json.load(f)
+    r = json.loads(subprocess.check_output([vlm_main, "params"], text=True, timeout=120))
+    assert r["params"] == g["vg_params"]
+    assert r["n_params"] == 357600
