@@ -55,3 +55,14 @@ def vlm_main(built, tmp_path_factory):
                            os.path.join(ROOT, "tests", "c", "vlm_main.c"), "-o", exe,
                            "-L" + libdir, "-ldnn_amd", "-Wl,-rpath," + libdir, "-lm"])
     return exe
+
+
+@pytest.fixture(scope="session")
+def ckpt_main(built, tmp_path_factory):
+    """tests/c/ckpt_main.c (module_save / module_load caller) built against libdnn_amd.so."""
+    exe = str(tmp_path_factory.mktemp("c") / "ckpt_main")
+    libdir = os.path.join(ROOT, "dnn.c_amd", "lib")
+    subprocess.check_call(["gcc", "-std=gnu11", "-O2", "-Wall", "-I" + os.path.join(ROOT, "include"),
+                           os.path.join(ROOT, "tests", "c", "ckpt_main.c"), "-o", exe,
+                           "-L" + libdir, "-ldnn_amd", "-Wl,-rpath," + libdir, "-lm"])
+    return exe

@@ -15,3 +15,7 @@ gcc -std=gnu11 -O2 -include stdint.h -I"$REF/include" -I"$REF/src" -w \
     tests/golden/gen_vlm.c -o oracle/_ref/gen_vlm \
     -Loracle/_ref -ldnnref -Wl,-rpath,"$PWD/oracle/_ref" -lm
 OMP_NUM_THREADS=1 ./oracle/_ref/gen_vlm
+gcc -std=gnu11 -O2 -include stdint.h -I"$REF/include" -I"$REF/src" -w \
+    tests/golden/gen_ckpt.c -o oracle/_ref/gen_ckpt \
+    -Loracle/_ref -ldnnref -Wl,-rpath,"$PWD/oracle/_ref" -lm
+OMP_NUM_THREADS=1 ./oracle/_ref/gen_ckpt

@@ -46,3 +46,20 @@ def test_vision_lm_weights_match_reference(vlm_main):
     r = json.loads(subprocess.check_output([vlm_main, "params"], text=True, timeout=120))
     assert r["params"] == g["vg_params"]
     assert r["n_params"] == 357600
+
+
+def test_dnnm_checkpoint_round_trip(ckpt_main, tmp_path):
+    """A DNNM checkpoint the reference's module_save wrote (module.c:208-230)
+    loads strictly into a model of other weights and gives the reference's
+    parameters bit for bit; module_save here writes the same bytes back, and
+    that file loads into a third model."""
+    with open(os.path.join(ROOT, "tests", "golden", "data", "ckpt.json")) as f:
+        g = json.load(f)
+    ref = os.path.join(ROOT, "tests", "golden", "data", "ckpt_small.dnnm")
+    out = str(tmp_path / "again.dnnm")
+    r = json.loads(subprocess.check_output([ckpt_main, "load", ref, out], text=True, timeout=120))
+    assert r["before"] != g["ckpt_params"]
+    assert r["loaded"] == g["ckpt_params"]
+    assert r["reloaded"] == g["ckpt_params"]
+    with open(ref, "rb") as a, open(out, "rb") as b:
+        assert a.read() == b.read()

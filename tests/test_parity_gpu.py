@@ -7,6 +7,7 @@ Bars:
     being max|dlogit| / max|logit| over the step's vocabulary row.
 """
 import json
+import os
 import subprocess
 
 import numpy as np
@@ -17,6 +18,8 @@ import oracle_lib as O
 from golden_util import binf
 
 pytestmark = pytest.mark.gpu
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 
 ABS_TOL = 1e-3
 REL_TOL = 1e-4
@@ -302,3 +305,16 @@ def test_c_api_nocache_and_sampling(generate_main, golden):
                                  "111", "16", "32", "0.8"], text=True, timeout=300)
     ra, rb = json.loads(a), json.loads(b)
     assert ra["tokens"] == rb["tokens"] and len(ra["tokens"]) == 48
+
+
+def test_checkpoint_load_then_generate(ckpt_main):
+    """Generate on a model's own weights (mirrored to HBM), module_load a
+    checkpoint the reference wrote, generate again: the device mirror follows
+    the new weights and the ids are the ones the reference generated from that
+    checkpoint."""
+    with open(os.path.join(ROOT, "tests", "golden", "data", "ckpt.json")) as f:
+        g = json.load(f)
+    ref = os.path.join(ROOT, "tests", "golden", "data", "ckpt_small.dnnm")
+    r = json.loads(subprocess.check_output([ckpt_main, "gen", ref], text=True, timeout=120))
+    assert r["loaded"] == g["ckpt_tokens"]
+    assert r["own"][:5] == g["ckpt_tokens"][:5] and r["own"] != g["ckpt_tokens"]
