@@ -36,6 +36,7 @@
 // order), and prefill (128 x 128 tiles, a 64 x 64 block per wavefront).
 
 #include "batch.h"
+#include <cstdlib>
 #include "decode_device.h"
 
 namespace dnnhip {
@@ -131,8 +132,9 @@ __device__ int g_btrace_step;
 #endif
 
 template <int MT, int NT, int WM, int WN, int KW, int KPW, bool BF, int EPI, bool NORM, bool AROW = false>
-__global__ __launch_bounds__(NTHR) void gemm_kernel(const GemmArgs g) {
-    static_assert(WM * WN * KW == 4, "four wavefronts");
+__global__ __launch_bounds__(64 * WM * WN * KW) void gemm_kernel(const GemmArgs g) {
+    static_assert(WM * WN * KW == 4 || WM * WN * KW == 8, "four or eight wavefronts");
+    constexpr int GT = 64 * WM * WN * KW;                  // threads
     constexpr int BM = 16 * MT * WM, BN = 16 * NT * WN;
     constexpr int LDR = BN + 1;
     constexpr int U = 4;                                   // k-steps per loop iteration (prefill shape)
@@ -215,13 +217,13 @@ __global__ __launch_bounds__(NTHR) void gemm_kernel(const GemmArgs g) {
 
     // decode shape: the epilogue's operands of this thread's column pairs,
     // loaded before the main loads so that they arrive with them
-    constexpr int EP = DEC ? (BM * BN / 2 + NTHR - 1) / NTHR : 1;
+    constexpr int EP = DEC ? (BM * BN / 2 + GT - 1) / GT : 1;
     float eb0[EP], eb1[EP], er0[EP], er1[EP], ecs[EP], esn[EP];
     int erb[EP], erp[EP];
     if constexpr (DEC) {
 #pragma unroll
         for (int e = 0; e < EP; e++) {
-            const int i = tid + e * NTHR;
+            const int i = tid + e * GT;
             const int m = i / (BN / 2), n = 2 * (i - m * (BN / 2));
             const int gm_ = tile_m * BM + m, gn = tile_n * BN + n;
             eb0[e] = eb1[e] = er0[e] = er1[e] = ecs[e] = esn[e] = 0.f;
@@ -271,7 +273,7 @@ __global__ __launch_bounds__(NTHR) void gemm_kernel(const GemmArgs g) {
             // RoPE entries of this thread's rows (their positions arrived first)
 #pragma unroll
             for (int e = 0; e < EP; e++) {
-                const int i = tid + e * NTHR;
+                const int i = tid + e * GT;
                 const int m = i / (BN / 2), n = 2 * (i - m * (BN / 2));
                 const int gm_ = tile_m * BM + m, gn = tile_n * BN + n;
                 if (i >= BM * BN / 2 || gm_ >= g.M || gn >= 2 * g.D) continue;
@@ -337,7 +339,7 @@ __global__ __launch_bounds__(NTHR) void gemm_kernel(const GemmArgs g) {
     const size_t n_main = (size_t)g.ks * g.M * g.N;
     const rsrc_t rp = buf(g.part, g.part ? (n_main + (size_t)gridDim.x * g.M) * 8 : 0);
     if (g.ks > 1) {
-        for (int i = tid; i < BM * BN / 2; i += NTHR) {
+        for (int i = tid; i < BM * BN / 2; i += GT) {
             const int m = i / (BN / 2), n = 2 * (i - m * (BN / 2));
             const int gm_ = tile_m * BM + m, gn = tile_n * BN + n;
             if (gm_ >= g.M || gn >= g.N) continue;
@@ -347,7 +349,7 @@ __global__ __launch_bounds__(NTHR) void gemm_kernel(const GemmArgs g) {
             st_pair2(rp, ((size_t)ksi * g.M + gm_) * g.N + gn, v0, v1, tag);
         }
         if (NORM)
-            for (int m = tid; m < BM; m += NTHR) {
+            for (int m = tid; m < BM; m += GT) {
                 const int gm_ = tile_m * BM + m;
                 if (gm_ >= g.M) continue;
                 float sv = 0.f;
@@ -359,7 +361,7 @@ __global__ __launch_bounds__(NTHR) void gemm_kernel(const GemmArgs g) {
         BTRACE(g.st, g.kslot, 3);
         if (NORM) {
             // the rows' sums of squares over all K, into ssl[0]
-            for (int m = tid; m < BM; m += NTHR) {
+            for (int m = tid; m < BM; m += GT) {
                 const int gm_ = tile_m * BM + m;
                 if (gm_ >= g.M) continue;
                 float sv = 0.f;
@@ -381,7 +383,7 @@ __global__ __launch_bounds__(NTHR) void gemm_kernel(const GemmArgs g) {
     // epilogue: two adjacent columns per thread
 #pragma unroll
     for (int e = 0; e < (DEC ? EP : 1); e++)
-    for (int i = tid + e * NTHR; i < BM * BN / 2; i += (DEC ? BM * BN : NTHR)) {
+    for (int i = tid + e * GT; i < BM * BN / 2; i += (DEC ? BM * BN : GT)) {
         const int m = i / (BN / 2), n = 2 * (i - m * (BN / 2));
         const int gm_ = tile_m * BM + m, gn = tile_n * BN + n;
         if (gm_ >= g.M || gn >= g.N) continue;
@@ -473,7 +475,7 @@ __global__ __launch_bounds__(NTHR) void gemm_kernel(const GemmArgs g) {
         // head_finish_kernel reduces the tiles after this launch
         __syncthreads();
         const int ntn = (g.N + BN - 1) / BN;
-        for (int m = tid; m < BM; m += NTHR) {
+        for (int m = tid; m < BM; m += GT) {
             const int gm_ = tile_m * BM + m;
             if (gm_ >= g.M) continue;
             float best = -INFINITY;
@@ -949,36 +951,57 @@ namespace {
 // decode shape: all rows in one tile (MT = rows / 16), k-steps per wavefront
 // KPW = K / 16 / (4 * ks), chosen by the host among the instantiated values
 template <int EPI, bool NORM, bool BF, int MT>
-hipError_t gemm_decode_mt(const GemmArgs &g, hipStream_t st, int kpw) {
+hipError_t gemm_decode_mt(const GemmArgs &g, hipStream_t st, int kw, int kpw) {
     const int ntn = (g.N + 15) / 16;
     dim3 grid(ntn * g.ks, (g.M + 16 * MT - 1) / (16 * MT));
-#define DNNHIP_KPW(K)                                                                                            \
+#define DNNHIP_KPW(KW, K)                                                                                        \
     case K:                                                                                                      \
         if (EPI == EPI_HEAD && g.arow)                                                                           \
-            hipLaunchKernelGGL((gemm_kernel<MT, 1, 1, 1, 4, K, BF, EPI, NORM, EPI == EPI_HEAD>), grid, dim3(NTHR), 0, st, g); \
+            hipLaunchKernelGGL((gemm_kernel<MT, 1, 1, 1, KW, K, BF, EPI, NORM, EPI == EPI_HEAD>), grid, dim3(64 * KW), 0, st, g); \
         else                                                                                                     \
-            hipLaunchKernelGGL((gemm_kernel<MT, 1, 1, 1, 4, K, BF, EPI, NORM>), grid, dim3(NTHR), 0, st, g);     \
+            hipLaunchKernelGGL((gemm_kernel<MT, 1, 1, 1, KW, K, BF, EPI, NORM>), grid, dim3(64 * KW), 0, st, g); \
         break;
-    switch (kpw) {
-        DNNHIP_KPW(2) DNNHIP_KPW(3) DNNHIP_KPW(4) DNNHIP_KPW(6) DNNHIP_KPW(8) DNNHIP_KPW(12)
-        default: return hipErrorInvalidValue;
+    if (kw == 8) {
+        switch (kpw) {
+            DNNHIP_KPW(8, 2) DNNHIP_KPW(8, 3) DNNHIP_KPW(8, 4) DNNHIP_KPW(8, 6) DNNHIP_KPW(8, 8)
+            default: return hipErrorInvalidValue;
+        }
+    } else {
+        switch (kpw) {
+            DNNHIP_KPW(4, 2) DNNHIP_KPW(4, 3) DNNHIP_KPW(4, 4) DNNHIP_KPW(4, 6) DNNHIP_KPW(4, 8) DNNHIP_KPW(4, 12)
+            default: return hipErrorInvalidValue;
+        }
     }
 #undef DNNHIP_KPW
     return hipGetLastError();
 }
 
+// Wavefronts splitting K in a decode GEMM workgroup: 8 where each then still
+// holds 2 to 8 k-blocks (half the MFMA chain and loads per wavefront of 4:
+// C3 60.4k -> 61.9k, C5 142k -> 149k tokens/s), else 4; DNN_HIP_GEMM_KW=4
+// keeps 4.
+int decode_kw(int nks, int ks) {
+    static const int forced = [] {
+        const char *e = getenv("DNN_HIP_GEMM_KW");
+        return e ? atoi(e) : 0;
+    }();
+    const bool eight_ok = nks % (8 * ks) == 0 && nks / (8 * ks) >= 2 && nks / (8 * ks) <= 8;
+    return forced != 4 && eight_ok ? 8 : 4;
+}
+
 template <int EPI, bool NORM, bool BF>
 hipError_t gemm_decode(const GemmArgs &g, hipStream_t st) {
     const int nks = g.K / 16;
-    if (nks % (4 * g.ks)) return hipErrorInvalidValue;
-    const int kpw = nks / (4 * g.ks);
+    const int kw = decode_kw(nks, g.ks);
+    if (nks % (kw * g.ks)) return hipErrorInvalidValue;
+    const int kpw = nks / (kw * g.ks);
     int mt = (g.M + 15) / 16;
     if (g.mt_max > 0 && mt > g.mt_max) mt = g.mt_max;     // row tiles per workgroup (the rest: more workgroups)
     switch (mt) {
-        case 1: return gemm_decode_mt<EPI, NORM, BF, 1>(g, st, kpw);
-        case 2: return gemm_decode_mt<EPI, NORM, BF, 2>(g, st, kpw);
-        case 3: return gemm_decode_mt<EPI, NORM, BF, 3>(g, st, kpw);
-        case 4: return gemm_decode_mt<EPI, NORM, BF, 4>(g, st, kpw);
+        case 1: return gemm_decode_mt<EPI, NORM, BF, 1>(g, st, kw, kpw);
+        case 2: return gemm_decode_mt<EPI, NORM, BF, 2>(g, st, kw, kpw);
+        case 3: return gemm_decode_mt<EPI, NORM, BF, 3>(g, st, kw, kpw);
+        case 4: return gemm_decode_mt<EPI, NORM, BF, 4>(g, st, kw, kpw);
         default: return hipErrorInvalidValue;
     }
 }
