@@ -31,9 +31,11 @@ CONFIGS = {
     "c1": (128, 256, 4, 4, 683, 16, 1),
     "c2": (8192, 768, 12, 12, 2048, 32, 1),
     "c3": (8192, 768, 12, 12, 2048, 32, 32),
+    "c2b2": (8192, 768, 12, 12, 2048, 32, 2),
+    "c2b4": (8192, 768, 12, 12, 2048, 32, 4),
     "c2b8": (8192, 768, 12, 12, 2048, 32, 8),
 }
-SEED = {"c1": 1, "c2": 2, "c3": 3, "c2b8": 2, "c4": 4, "c5": 5}
+SEED = {"c1": 1, "c2": 2, "c3": 3, "c2b2": 2, "c2b4": 2, "c2b8": 2, "c4": 4, "c5": 5}
 KERNELS = {3: "decode_v3<NB,DC>", 4: "decode_v4<NB,DC>", 5: "decode_v5<NB,DC>",
            6: "batched engine: gemm_kernel / attn_kernel chain, one HIP graph replay per step"}
 

@@ -324,8 +324,13 @@ int dnn_hip_session_create(dnn_hip_model *m, int B, int max_seq, dnn_hip_session
     s->h_pos.assign(B, 0);
     if (const char *k = getenv("DNN_HIP_DECODE_KERNEL")) s->kernel_pref = atoi(k);
     if (const char *k = getenv("DNN_HIP_ATT_SPLITS")) s->att_splits_req = atoi(k);
-    // more than MAXB rows, bf16 weights, or on request: the batched engine
-    s->batched = B > MAXB || m->bf16 || s->kernel_pref == 6;
+    // the batched engine for more than 4 rows (from 5 rows on it beats the
+    // persistent kernel, which runs 5-8 rows at its 8-row cost: C2 at 8 rows
+    // 17.8k vs 15.4k tokens/s, 1,024-key histories 14.5k vs 11.5k), bf16
+    // weights, or on request; DNN_HIP_DECODE_KERNEL=3/4/5 keeps up to 8 rows
+    // on the persistent kernels
+    const bool persistent_pref = s->kernel_pref >= 3 && s->kernel_pref <= 5;
+    s->batched = B > MAXB || m->bf16 || s->kernel_pref == 6 || (B > 4 && !persistent_pref);
     int n_cu = 0;
     if (hipDeviceGetAttribute(&n_cu, hipDeviceAttributeMultiprocessorCount, m->device) != hipSuccess || n_cu <= 0) n_cu = 256;
     s->grid_cap = n_cu;

@@ -98,10 +98,11 @@ int dnn_hip_model_destroy(dnn_hip_model *m);
 /* A decode session: the per-layer KV caches of `batch` rows in HBM (K stored
  * transposed, [L][B][H][d_k][max_seq]; V as [L][B][H][max_seq][d_k]) plus the
  * exchange arena of the decode kernel.  Every row starts empty.
- * 1 <= batch <= 64.  Sessions of at most 8 rows decode with one persistent
- * kernel launch per call; sessions of more rows (and every session of a bf16
- * model) decode on the batched engine, one replay of a captured HIP graph per
- * step, every weight read once per step for all rows. */
+ * 1 <= batch <= 64.  Sessions of at most 4 fp32 rows decode with one
+ * persistent kernel launch per call; sessions of more rows (and every session
+ * of a bf16 model) decode on the batched engine, one replay of a captured HIP
+ * graph per step, every weight read once per step for all rows (the
+ * persistent kernel takes up to 8 rows when DNN_HIP_DECODE_KERNEL=3). */
 int dnn_hip_session_create(dnn_hip_model *m, int batch, int max_seq,
                            dnn_hip_session **out);
 /* Empties every row (lengths back to 0). */
@@ -196,11 +197,12 @@ int dnn_hip_session_set_grid(dnn_hip_session *s, int n_workgroups);
 /* Workgroups the last dnn_hip_decode launch on this session used. */
 int dnn_hip_session_grid(dnn_hip_session *s, int *n_workgroups);
 /* Which decode kernel the last dnn_hip_decode launch used: 3 = the general
- * persistent one (up to 8 rows, the default), 4 = the layer-lookahead kernel,
- * 5 = the streaming kernel (both 1-2 rows), chosen when the environment variable
+ * persistent one (up to 4 rows by default, up to 8 when
+ * DNN_HIP_DECODE_KERNEL=3), 4 = the layer-lookahead kernel, 5 = the streaming
+ * kernel (both 1-2 rows), chosen when the environment variable
  * DNN_HIP_DECODE_KERNEL is 4 or 5 at session creation and the kernel's
- * schedule fits the model and grid; 6 = the batched engine (more than 8 rows,
- * bf16 weights, or DNN_HIP_DECODE_KERNEL=6). */
+ * schedule fits the model and grid; 6 = the batched engine (more rows, bf16
+ * weights, or DNN_HIP_DECODE_KERNEL=6). */
 int dnn_hip_session_kernel(dnn_hip_session *s, int *which);
 /* Workgroups per (row, head) over which the last general-kernel (3) launch split
  * each head's cached keys (1 = unsplit; chosen from the launch's longest

@@ -103,10 +103,13 @@ def test_c2_gpt2_init_tokens(golden):
     assert list(out) == want
 
 
-@pytest.mark.parametrize("B", [2, 5, 8, 20])
-def test_batch_rows_match_independent_runs(c1g, B):
+@pytest.mark.parametrize("B,kern", [(2, ""), (5, ""), (5, "3"), (8, ""), (8, "3"), (20, "")])
+def test_batch_rows_match_independent_runs(c1g, monkeypatch, B, kern):
     """Each row of a batched decode equals its own B=1 run (rows differ in
-    prompt length, so they switch from prompt to greedy at different steps)."""
+    prompt length, so they switch from prompt to greedy at different steps);
+    5 and 8 rows on the default (batched engine) and on the persistent kernel."""
+    if kern:
+        monkeypatch.setenv("DNN_HIP_DECODE_KERNEL", kern)
     hm = hip_model(c1g)
     rng = np.random.default_rng(B)
     lens = rng.integers(1, 9, size=B).astype(np.int32)
@@ -120,6 +123,7 @@ def test_batch_rows_match_independent_runs(c1g, B):
         assert got == list(want), "row %d" % b
         assert_logits_close(lg[lens[b] - 1:, b], wlg, "row %d" % b)
     assert list(s.lengths()) == [steps] * B
+    assert s.kernel() == (3 if B <= 4 or kern == "3" else 6)
 
 
 @pytest.mark.parametrize("B", [1, 2])
