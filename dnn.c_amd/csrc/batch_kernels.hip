@@ -549,10 +549,12 @@ __global__ __launch_bounds__(FIN_THR) void head_finish_kernel(const GemmArgs g) 
     }
     if (done) return;
     __syncthreads();                                   // s_all initialised
+    // every row's token first, then every next-step embedding load, then the
+    // stores (a store could alias a later load: interleaved, each row's copy
+    // would wait for the previous row's)
+    int tokr[FIN_ROWS];
 #pragma unroll
     for (int r = 0; r < FIN_ROWS; r++) {
-        const int m = w + 16 * r;
-        if (m >= g.M) continue;
         float bv = best[r];
         int bx = bi[r];
 #pragma unroll
@@ -561,7 +563,24 @@ __global__ __launch_bounds__(FIN_THR) void head_finish_kernel(const GemmArgs g) 
             const int oi = __shfl_xor(bx, o);
             if (ov > bv || (ov == bv && oi < bx)) { bv = ov; bx = oi; }
         }
-        const int tok = bx == 0x7fffffff ? 0 : bx;
+        tokr[r] = bx == 0x7fffffff ? 0 : bx;
+    }
+    constexpr int CPL = BK_MAXD / 64;
+    float ev[FIN_ROWS][CPL];
+#pragma unroll
+    for (int r = 0; r < FIN_ROWS; r++) {
+        const int m = w + 16 * r;
+        const int nxt = fnext[r] >= 0 ? fnext[r] : tokr[r];
+        const float *e = g.embed + (size_t)nxt * g.ldx;
+        const bool live = !g.prefill && m < g.M;
+#pragma unroll
+        for (int j = 0; j < CPL; j++) ev[r][j] = (live && lane + 64 * j < g.D) ? e[lane + 64 * j] : 0.f;
+    }
+#pragma unroll
+    for (int r = 0; r < FIN_ROWS; r++) {
+        const int m = w + 16 * r;
+        if (m >= g.M) continue;
+        const int tok = tokr[r];
         if (g.prefill) {
             if (lane == 0) g.ids[m] = tok;
             continue;
@@ -575,19 +594,11 @@ __global__ __launch_bounds__(FIN_THR) void head_finish_kernel(const GemmArgs g) 
             g.row_done[m] = dr;
             if (!dr) atomicAnd(&s_all, 0);
         }
-        // the next step's embedding row (embedding.c:79-84): every load of the
-        // row before the first store (a store may alias a later load, which
-        // would otherwise serialise the copy)
-        const int nxt = fnext[r] >= 0 ? fnext[r] : tok;
-        const float *e = g.embed + (size_t)nxt * g.ldx;
-        constexpr int CPL = BK_MAXD / 64;
-        float ev[CPL];
-#pragma unroll
-        for (int j = 0; j < CPL; j++) ev[j] = (lane + 64 * j < g.D) ? e[lane + 64 * j] : 0.f;
+        // the next step's embedding row (embedding.c:79-84)
 #pragma unroll
         for (int j = 0; j < CPL; j++) {
             const int c = lane + 64 * j;
-            if (c < g.D) g.x_next[g.pk ? pk_index(m, c, g.ldx) : (size_t)m * g.ldx + c] = ev[j];
+            if (c < g.D) g.x_next[g.pk ? pk_index(m, c, g.ldx) : (size_t)m * g.ldx + c] = ev[r][j];
         }
     }
     __syncthreads();
