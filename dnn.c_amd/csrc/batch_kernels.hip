@@ -547,8 +547,10 @@ __global__ __launch_bounds__(FIN_THR) void head_finish_kernel(const GemmArgs g) 
                 if (v > best[r] || (v == best[r] && idx < bi[r])) { best[r] = v; bi[r] = idx; }
             }
     }
+    BTRACE(g.st, g.kslot + 1, 2);
     if (done) return;
     __syncthreads();                                   // s_all initialised
+    BTRACE(g.st, g.kslot + 1, 3);
     // every row's token first, then every next-step embedding load, then the
     // stores (a store could alias a later load: interleaved, each row's copy
     // would wait for the previous row's)
@@ -565,16 +567,20 @@ __global__ __launch_bounds__(FIN_THR) void head_finish_kernel(const GemmArgs g) 
         }
         tokr[r] = bx == 0x7fffffff ? 0 : bx;
     }
-    constexpr int CPL = BK_MAXD / 64;
-    float ev[FIN_ROWS][CPL];
+    // four columns per lane and load: the arena's embedding rows are zero past
+    // D, so the last group may cover padding columns (X holds zeros there too)
+    constexpr int CPL = BK_MAXD / 256;
+    static_assert(BK_MAXD % 256 == 0, "whole float4 groups per lane");
+    float4 ev[FIN_ROWS][CPL];
 #pragma unroll
     for (int r = 0; r < FIN_ROWS; r++) {
         const int m = w + 16 * r;
         const int nxt = fnext[r] >= 0 ? fnext[r] : tokr[r];
-        const float *e = g.embed + (size_t)nxt * g.ldx;
+        const float4 *e = reinterpret_cast<const float4 *>(g.embed + (size_t)nxt * g.ldx);
         const bool live = !g.prefill && m < g.M;
 #pragma unroll
-        for (int j = 0; j < CPL; j++) ev[r][j] = (live && lane + 64 * j < g.D) ? e[lane + 64 * j] : 0.f;
+        for (int j = 0; j < CPL; j++)
+            ev[r][j] = (live && 4 * (lane + 64 * j) < g.D) ? e[lane + 64 * j] : make_float4(0.f, 0.f, 0.f, 0.f);
     }
 #pragma unroll
     for (int r = 0; r < FIN_ROWS; r++) {
@@ -597,10 +603,12 @@ __global__ __launch_bounds__(FIN_THR) void head_finish_kernel(const GemmArgs g) 
         // the next step's embedding row (embedding.c:79-84)
 #pragma unroll
         for (int j = 0; j < CPL; j++) {
-            const int c = lane + 64 * j;
-            if (c < g.D) g.x_next[g.pk ? pk_index(m, c, g.ldx) : (size_t)m * g.ldx + c] = ev[r][j];
+            const int c = 4 * (lane + 64 * j);
+            if (c < g.D)
+                *reinterpret_cast<float4 *>(g.x_next + (g.pk ? pk_index(m, c, g.ldx) : (size_t)m * g.ldx + c)) = ev[r][j];
         }
     }
+    BTRACE(g.st, g.kslot + 1, 4);
     __syncthreads();
     BTRACE(g.st, g.kslot + 1, 1);
     if (tid == 0) {
