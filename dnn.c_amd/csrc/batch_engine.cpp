@@ -60,9 +60,18 @@ int pick_ks(int ntiles, int K, int M, bool norm, int mt_max = 0) {
     return best;
 }
 
-// workgroups per (row, head) of the decode attention: one where the rows and
-// heads alone fill the chip
-int attn_splits(int M, int H) { return M * H >= 256 ? 1 : std::min(8, (256 + M * H - 1) / (M * H)); }
+// workgroups per (row, head) of the decode attention over histories of up to
+// S_max keys: one where the rows and heads alone fill the chip, else the fewest
+// that leave each wavefront at most two 64-key chunks (a split's merge -- the
+// partials, the counter and the last arriver's reload -- costs more than a
+// wider launch gains: measured on 8 rows of 32..1087 keys); at most 8.
+// DNN_HIP_ATT_SPLITS overrides.
+int attn_splits(const dnn_hip_session *s, int M, int H, int S_max) {
+    if (s->att_splits_req > 0) return std::min(8, s->att_splits_req);
+    if (M * H >= 256) return 1;
+    const int aw = attn_waves(M, H), nch = (S_max + 63) / 64;
+    return std::max(1, std::min(8, (nch + 2 * aw - 1) / (2 * aw)));
+}
 
 // Split-K partial pairs a decode GEMM of these dimensions needs.
 size_t part_pairs_for(int N, int K, int M, bool norm, int mt_max = 0) {
@@ -287,7 +296,7 @@ int enqueue_layer(dnn_hip_session *s, int l, const PrefillPlan *pp) {
         AttnArgs a{};
         a.q = e->Q; a.att = e->ATT; a.kc = s->kc; a.vc = s->vc; a.pos = s->pos;
         a.M = M; a.H = m->H; a.kv_s = s->kv_s; a.layer = l; a.D = D; a.B = s->B; a.ldatt = ldD;
-        a.nsplit = attn_splits(M, m->H);
+        a.nsplit = e->att_ns;
         a.part = e->apart; a.cnt = e->cnt + CNT_GEMM; a.st = e->st; a.kslot = 5 * l + 1;
         a.pk = 1;                               // decode steps: ATT in fragment order
         a.spec = e->att_spec;
@@ -392,7 +401,11 @@ int engine_decode(dnn_hip_session *s, const int *feed, int n_feed_all, const int
     // first chunk (64 keys of split 0) at least 3/4 of this call's (row, step)
     // pairs have, at least one
     {
-        const int ns = attn_splits(B, m->H);
+        int s_max = 0;
+        for (int b = 0; b < B; b++) s_max = std::max(s_max, s->h_pos[b] + n_steps);
+        const int ns = attn_splits(s, B, m->H, s_max);
+        e->att_ns = ns;
+        s->att_splits = ns;
         int spec = 1;
         for (int w = 1; w < 4; w++) {
             const long long keys = 64LL * ns * w;
@@ -410,7 +423,8 @@ int engine_decode(dnn_hip_session *s, const int *feed, int n_feed_all, const int
     // parameter changed
     float *lg = logits ? s->logits : nullptr;
     const void *key[4] = {s->feed, s->ids, lg, e->X};
-    if (!e->gexec || e->geos != eos || e->gspec != e->att_spec || memcmp(key, e->gkey, sizeof key) != 0) {
+    if (!e->gexec || e->geos != eos || e->gspec != e->att_spec || e->gns != e->att_ns ||
+        memcmp(key, e->gkey, sizeof key) != 0) {
         drop_graph(e);
         HIP_TRY(hipStreamBeginCapture(s->stream, hipStreamCaptureModeThreadLocal));
         int erc = 0;
@@ -426,6 +440,7 @@ int engine_decode(dnn_hip_session *s, const int *feed, int n_feed_all, const int
         memcpy(e->gkey, key, sizeof key);
         e->geos = eos;
         e->gspec = e->att_spec;
+        e->gns = e->att_ns;
     }
     // the first step's embedding rows; resets the step counter, done flags
     EmbedArgs ea{};

@@ -1112,7 +1112,7 @@ hipError_t launch_attn(const AttnArgs &a, hipStream_t stream) {
     // eight wavefronts per (row, head, split) when there are few of them (one
     // workgroup per CU at this register use: every chunk of up to 512 keys in
     // one round), four otherwise (two workgroups per CU)
-    if (a.M * a.H <= 128)
+    if (attn_waves(a.M, a.H) == 8)
         hipLaunchKernelGGL(attn_kernel<8>, dim3(a.M * a.H * a.nsplit), dim3(512), 0, stream, a);
     else
         hipLaunchKernelGGL(attn_kernel<4>, dim3(a.M * a.H * a.nsplit), dim3(256), 0, stream, a);

@@ -63,6 +63,8 @@ struct BatchEngine {
     const void *gkey[4] = {nullptr, nullptr, nullptr, nullptr};
     int att_spec = 4;                // decode attention: wavefronts that load before the row length is known
     int gspec = -1;                  // att_spec of the captured step graph
+    int att_ns = 1;                  // decode attention: workgroups per (row, head)
+    int gns = -1;                    // att_ns of the captured step graph
     int geos = -2;
 };
 

@@ -204,10 +204,10 @@ int dnn_hip_session_grid(dnn_hip_session *s, int *n_workgroups);
  * schedule fits the model and grid; 6 = the batched engine (more rows, bf16
  * weights, or DNN_HIP_DECODE_KERNEL=6). */
 int dnn_hip_session_kernel(dnn_hip_session *s, int *which);
-/* Workgroups per (row, head) over which the last general-kernel (3) launch split
- * each head's cached keys (1 = unsplit; chosen from the launch's longest
- * history, or fixed by the environment variable DNN_HIP_ATT_SPLITS at session
- * creation). */
+/* Workgroups per (row, head) over which the last decode call split each
+ * head's cached keys, on the general kernel (3) or the batched engine (6); 1 on
+ * the other kernels (1 = unsplit; chosen from the call's longest history, or
+ * fixed by the environment variable DNN_HIP_ATT_SPLITS at session creation). */
 int dnn_hip_session_att_splits(dnn_hip_session *s, int *splits);
 
 #ifdef __cplusplus

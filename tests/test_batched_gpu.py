@@ -22,19 +22,24 @@ def c1g():
     return O.Model(128, 256, 4, 4, 683, 256, seed=11, init="gpt2")
 
 
-@pytest.mark.parametrize("B", [16, 33, 64])
-def test_engine_rows_match_independent_runs(c1g, B):
+@pytest.mark.parametrize("B,splits", [(16, None), (33, None), (64, None), (16, 3), (12, 8)])
+def test_engine_rows_match_independent_runs(c1g, B, splits, monkeypatch):
     """Every row of a batched decode (the engine: more than 8 rows) equals its
-    own B=1 oracle run; rows switch from prompt to greedy at different steps."""
+    own B=1 oracle run; rows switch from prompt to greedy at different steps.
+    With `splits` (DNN_HIP_ATT_SPLITS) each head's keys are split over that
+    many workgroups and merged by the last one to arrive."""
+    if splits:
+        monkeypatch.setenv("DNN_HIP_ATT_SPLITS", str(splits))
     hm = hip_model(c1g)
     rng = np.random.default_rng(100 + B)
     lens = rng.integers(1, 9, size=B).astype(np.int32)
     feed = rng.integers(0, 128, size=(8, B)).astype(np.int32)
     steps = 40
-    print("engine rows B=%d" % B, flush=True)
+    print("engine rows B=%d splits=%s" % (B, splits), flush=True)
     s = A.HipSession(hm, B, 72)
     ids, lg = s.decode(feed, steps, n_feed=lens, want_logits=True)
     assert s.kernel() == 6
+    assert s.att_splits() == (splits or 1)
     for b in range(B):
         want, wlg = c1g.generate(feed[: lens[b], b], steps - lens[b] + 1, eos=-1, want_logits=True)
         got = list(feed[: lens[b], b]) + list(ids[lens[b] - 1:, b])
@@ -81,6 +86,28 @@ def test_engine_equals_persistent_kernel_c2_b8(golden, monkeypatch):
     assert np.array_equal(ids3, ids6)
     for b in range(8):
         assert_logits_close(lg6[:, b], lg3[:, b], "row %d" % b)
+
+
+def test_engine_long_history_splits(monkeypatch):
+    """Six rows past 1,024 cached keys: the engine splits each head's keys over
+    two workgroups (at most two 64-key chunks per wavefront of eight) and the
+    tokens and logits still follow the oracle's generation from each prompt."""
+    monkeypatch.delenv("DNN_HIP_ATT_SPLITS", raising=False)
+    m = O.Model(128, 256, 4, 4, 683, 1100, seed=11, init="gpt2")
+    hm = hip_model(m)
+    B, steps = 6, 12
+    rng = np.random.default_rng(61)
+    n = rng.integers(1030, 1061, size=B).astype(np.int32)
+    ids = rng.integers(0, 128, size=(B, int(n.max()))).astype(np.int32)
+    print("engine long history n=%s" % list(n), flush=True)
+    s = A.HipSession(hm, B, 1100)
+    nxt, _ = s.prefill(ids=ids, n_ids=n)
+    out, lg = s.decode(nxt, steps, want_logits=True)
+    assert s.kernel() == 6 and s.att_splits() == 2
+    for b in range(B):
+        want, wlg = m.generate(ids[b, : n[b]], steps + 1, eos=-1, want_logits=True)
+        assert [int(nxt[b])] + list(out[:, b]) == list(want[n[b]:]), "row %d" % b
+        assert_logits_close(lg[:, b], wlg[1:], "row %d" % b)
 
 
 @pytest.mark.parametrize("B", [1, 5, 12])
