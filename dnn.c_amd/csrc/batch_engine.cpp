@@ -83,6 +83,15 @@ int norm_mt(const char *env, int M, bool qkv) {
     return qkv && (M + 15) / 16 <= 2 ? 1 : 2;
 }
 
+// Row tiles per workgroup of the decode down GEMM (one, as out_proj: 64 rows
+// 160k -> 169k tokens/s, 32 rows unchanged) and lm_head GEMM (all rows: one
+// per workgroup was slower at 32 and 64 rows); DNN_HIP_DOWN_MT /
+// DNN_HIP_HEAD_MT override (0: all rows).
+int plain_mt(const char *env, int dflt) {
+    const char *v = getenv(env);
+    return v ? atoi(v) : dflt;
+}
+
 // Split-K partial pairs a decode GEMM of these dimensions needs.
 size_t part_pairs_for(int N, int K, int M, bool norm, int mt_max = 0) {
     const int ntn = (N + 15) / 16, ks = pick_ks(ntn, K, M, norm, mt_max);
@@ -179,8 +188,8 @@ int engine_get(dnn_hip_session *s, int rows, int layout = 0) {
         for (int rows = 16; rows <= MAX_ROWS; rows += 16) {
             const size_t need[5] = {part_pairs_for(3 * m->D, m->ldD, rows, true, norm_mt("DNN_HIP_QKV_MT", rows, true)),
                                     part_pairs_for(m->D, m->ldD, rows, false, 1),
-                                    part_pairs_for(2 * m->F, m->ldD, rows, true, norm_mt("DNN_HIP_GU_MT", rows, false)), part_pairs_for(m->D, m->ldF, rows, false),
-                                    part_pairs_for(m->V, m->ldD, rows, true)};
+                                    part_pairs_for(2 * m->F, m->ldD, rows, true, norm_mt("DNN_HIP_GU_MT", rows, false)), part_pairs_for(m->D, m->ldF, rows, false, plain_mt("DNN_HIP_DOWN_MT", 1)),
+                                    part_pairs_for(m->V, m->ldD, rows, true, plain_mt("DNN_HIP_HEAD_MT", 0))};
             for (size_t n : need) e->part_pairs = std::max(e->part_pairs, n);
         }
         e->apart_pairs = (size_t)MAX_ROWS * m->H * 8 * (BK_DK + 2);
@@ -341,7 +350,8 @@ int enqueue_layer(dnn_hip_session *s, int l, const PrefillPlan *pp) {
     g.A = e->ACT; g.lda = ldF; g.M = M;
     g.bias = W.f(lo.bd);
     g.out = e->X; g.ldo = ldD; g.res = e->X1; g.ldr = ldD;
-    g.ks = pre ? 1 : pick_ks((D + 15) / 16, ldF, M, false);
+    if (!pre) g.mt_max = plain_mt("DNN_HIP_DOWN_MT", 1);
+    g.ks = pre ? 1 : pick_ks((D + 15) / 16, ldF, M, false, g.mt_max);
     g.part = e->part; g.cnt = e->cnt; g.kslot = 5 * l + 4;
     g.pk = !pre;
     HIP_TRY(launch_gemm(EPI_RES, false, bf, pre, g, s->stream));
@@ -369,7 +379,8 @@ int enqueue_head(dnn_hip_session *s, const PrefillPlan *pp, float *logits, int *
     g.prefill = pp != nullptr;
     g.pk = pp == nullptr;                    // decode steps: X in fragment order
     g.kslot = 5 * m->L;
-    g.ks = pick_ks((m->V + 15) / 16, m->ldD, g.M, true);
+    if (!pp) g.mt_max = plain_mt("DNN_HIP_HEAD_MT", 0);
+    g.ks = pick_ks((m->V + 15) / 16, m->ldD, g.M, true, g.mt_max);
     g.amax_tiles = (m->V + 15) / 16;
     g.part = e->part; g.cnt = e->cnt;
     HIP_TRY(launch_gemm(EPI_HEAD, norm, m->bf16 != 0, false, g, s->stream));
