@@ -74,13 +74,14 @@ int attn_splits(const dnn_hip_session *s, int M, int H, int S_max) {
 }
 
 // Row tiles per workgroup of the decode QKV and gate/up GEMMs (rms_norm fused,
-// not split over K): at most two, so 48-64 rows launch the column tiles'
-// workgroups twice over, and one for the QKV GEMM of up to 32 rows (measured:
-// 64 rows 149k -> 160k tokens/s, 32 rows +0.5%; one for gate/up at 32 rows was
-// slower).  DNN_HIP_QKV_MT / DNN_HIP_GU_MT override (0: all rows).
+// not split over K): one for QKV, so every 16 rows launch the column tiles'
+// workgroups again; one for gate/up from 33 rows on, all rows below (measured:
+// 64 rows 149k -> 179k tokens/s with the down GEMM's single tile, 32 rows QKV
+// +0.5%, gate/up at one tile 1% slower).  DNN_HIP_QKV_MT / DNN_HIP_GU_MT
+// override (0: all rows).
 int norm_mt(const char *env, int M, bool qkv) {
     if (const char *v = getenv(env)) return atoi(v);
-    return qkv && (M + 15) / 16 <= 2 ? 1 : 2;
+    return qkv || (M + 15) / 16 > 2 ? 1 : 0;
 }
 
 // Row tiles per workgroup of the decode down GEMM (one, as out_proj: 64 rows
