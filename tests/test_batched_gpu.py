@@ -22,20 +22,30 @@ def c1g():
     return O.Model(128, 256, 4, 4, 683, 256, seed=11, init="gpt2")
 
 
-@pytest.mark.parametrize("B,splits", [(16, None), (33, None), (64, None), (16, 3), (12, 8)])
-def test_engine_rows_match_independent_runs(c1g, B, splits, monkeypatch):
+# the GEMMs' row tiles per workgroup away from the defaults: two (QKV, gate/up),
+# all rows (down), one (lm_head)
+TILES = {"DNN_HIP_QKV_MT": "2", "DNN_HIP_GU_MT": "2", "DNN_HIP_DOWN_MT": "0", "DNN_HIP_HEAD_MT": "1"}
+
+
+@pytest.mark.parametrize("B,splits,tiles", [(16, None, False), (33, None, False), (64, None, False),
+                                            (16, 3, False), (12, 8, False), (64, None, True), (48, None, True)])
+def test_engine_rows_match_independent_runs(c1g, B, splits, tiles, monkeypatch):
     """Every row of a batched decode (the engine: more than 8 rows) equals its
     own B=1 oracle run; rows switch from prompt to greedy at different steps.
     With `splits` (DNN_HIP_ATT_SPLITS) each head's keys are split over that
-    many workgroups and merged by the last one to arrive."""
+    many workgroups and merged by the last one to arrive; with `tiles` the
+    GEMMs take other row tiles per workgroup than the defaults."""
     if splits:
         monkeypatch.setenv("DNN_HIP_ATT_SPLITS", str(splits))
+    if tiles:
+        for k, v in TILES.items():
+            monkeypatch.setenv(k, v)
     hm = hip_model(c1g)
     rng = np.random.default_rng(100 + B)
     lens = rng.integers(1, 9, size=B).astype(np.int32)
     feed = rng.integers(0, 128, size=(8, B)).astype(np.int32)
     steps = 40
-    print("engine rows B=%d splits=%s" % (B, splits), flush=True)
+    print("engine rows B=%d splits=%s tiles=%s" % (B, splits, tiles), flush=True)
     s = A.HipSession(hm, B, 72)
     ids, lg = s.decode(feed, steps, n_feed=lens, want_logits=True)
     assert s.kernel() == 6
