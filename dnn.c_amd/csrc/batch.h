@@ -75,7 +75,9 @@ struct GemmArgs {
     int rope_rows;
     // split-K partials and last-arriver counters
     uint2 *part;                // [ks][M][N] tagged pairs, then [column tiles][ks][M] row sums of squares
-    unsigned *cnt;              // per column tile
+    size_t part_cap;            // pairs the part buffer holds (a launch needing more is refused)
+    unsigned *cnt;              // per (row group, column tile)
+    int cnt_cap;                // counters at cnt (a launch needing more is refused)
     StepState *st;
     int kslot;                  // distinct per launch of a step: tags are tag * 128 + kslot
     // HEAD

@@ -99,6 +99,39 @@ size_t part_pairs_for(int N, int K, int M, bool norm, int mt_max = 0) {
     return ks > 1 ? (size_t)ks * M * N + (size_t)ntn * ks * M : 0;
 }
 
+// Row tiles per workgroup (mt_max) of each decode-shape GEMM, as the launches
+// use them: the layer GEMMs of decode steps, and the lm_head of decode steps
+// (head_decode) or of prefill / dnn_hip_head_forward (all rows).
+struct MtPlan {
+    int qkv, out, gu, down, head;
+};
+MtPlan mt_plan(int M, bool head_decode) {
+    MtPlan p;
+    p.qkv = norm_mt("DNN_HIP_QKV_MT", M, true);
+    p.out = 1;                       // out_proj: one 16-row tile per workgroup (more, lighter workgroups)
+    p.gu = norm_mt("DNN_HIP_GU_MT", M, false);
+    p.down = plain_mt("DNN_HIP_DOWN_MT", 1);
+    p.head = head_decode ? plain_mt("DNN_HIP_HEAD_MT", 0) : 0;
+    return p;
+}
+
+// Split-K partial pairs of the engine: the largest need of any decode-shape
+// GEMM launch at any row count (the prefill GEMMs never split K).
+size_t engine_part_pairs(const dnn_hip_model *m) {
+    size_t need = 1;
+    for (int rows = 1; rows <= MAX_ROWS; rows++)
+        for (int hd = 0; hd < 2; hd++) {
+            const MtPlan p = mt_plan(rows, hd != 0);
+            const size_t n[5] = {part_pairs_for(3 * m->D, m->ldD, rows, true, p.qkv),
+                                 part_pairs_for(m->D, m->ldD, rows, false, p.out),
+                                 part_pairs_for(2 * m->F, m->ldD, rows, true, p.gu),
+                                 part_pairs_for(m->D, m->ldF, rows, false, p.down),
+                                 part_pairs_for(m->V, m->ldD, rows, true, p.head)};
+            for (size_t v : n) need = std::max(need, v);
+        }
+    return need;
+}
+
 void free_acts(BatchEngine *e) {
     float *bufs[] = {e->X, e->X1, e->ATT, e->Q, e->ACT};
     for (float *p : bufs)
@@ -185,14 +218,7 @@ int engine_get(dnn_hip_session *s, int rows, int layout = 0) {
     if (!e) {
         e = s->eng = new BatchEngine();
         const int ntn_head = (m->V + 15) / 16;
-        e->part_pairs = 1;
-        for (int rows = 16; rows <= MAX_ROWS; rows += 16) {
-            const size_t need[5] = {part_pairs_for(3 * m->D, m->ldD, rows, true, norm_mt("DNN_HIP_QKV_MT", rows, true)),
-                                    part_pairs_for(m->D, m->ldD, rows, false, 1),
-                                    part_pairs_for(2 * m->F, m->ldD, rows, true, norm_mt("DNN_HIP_GU_MT", rows, false)), part_pairs_for(m->D, m->ldF, rows, false, plain_mt("DNN_HIP_DOWN_MT", 1)),
-                                    part_pairs_for(m->V, m->ldD, rows, true, plain_mt("DNN_HIP_HEAD_MT", 0))};
-            for (size_t n : need) e->part_pairs = std::max(e->part_pairs, n);
-        }
+        e->part_pairs = engine_part_pairs(m);
         e->apart_pairs = (size_t)MAX_ROWS * m->H * 8 * (BK_DK + 2);
         e->amax_pairs = (size_t)MAX_ROWS * ntn_head;
         int rc = 0;
@@ -269,6 +295,8 @@ GemmArgs gemm_base(dnn_hip_session *s, const Wts &W, uint32_t woff, size_t pk, i
     g.st = s->eng->st;
     g.mpad = s->eng->mcap;
     g.D = s->m->D;
+    g.part_cap = s->eng->part_pairs;
+    g.cnt_cap = CNT_GEMM;
     return g;
 }
 
@@ -290,10 +318,11 @@ int enqueue_layer(dnn_hip_session *s, int l, const PrefillPlan *pp) {
     const bool pre = pp != nullptr;
     const int M = pre ? pp->M : s->B;
     const bool bf = m->bf16 != 0;
+    const MtPlan mp = mt_plan(M, true);
 
     GemmArgs g = gemm_base(s, W, lo.wqkv, m->pk_l[(size_t)l * 4 + 0], ldD, 3 * D, ldD);
     g.A = e->X; g.lda = ldD; g.M = M;
-    if (!pre) g.mt_max = norm_mt("DNN_HIP_QKV_MT", M, true);
+    if (!pre) g.mt_max = mp.qkv;
     g.ks = pre ? 1 : pick_ks((3 * D + 15) / 16, ldD, M, true, g.mt_max);
     g.part = e->part; g.cnt = e->cnt;
     g.bias = W.f(lo.bqkv);
@@ -329,7 +358,7 @@ int enqueue_layer(dnn_hip_session *s, int l, const PrefillPlan *pp) {
     g.A = e->ATT; g.lda = ldD; g.M = M;
     g.bias = W.f(lo.bo);
     g.out = e->X1; g.ldo = ldD; g.res = e->X; g.ldr = ldD;
-    g.mt_max = 1;          // out_proj: one 16-row tile per workgroup (more, lighter workgroups)
+    if (!pre) g.mt_max = mp.out;
     g.ks = pre ? 1 : pick_ks((D + 15) / 16, ldD, M, false, g.mt_max);
     g.part = e->part; g.cnt = e->cnt; g.kslot = 5 * l + 2;
     g.pk = !pre;
@@ -340,7 +369,7 @@ int enqueue_layer(dnn_hip_session *s, int l, const PrefillPlan *pp) {
     g.bias = W.f(lo.bg); g.bias2 = W.f(lo.bu);
     g.gamma = W.f(lo.g_ffn); g.eps = lo.eps_ffn; g.dnorm = D;
     g.out = e->ACT; g.ldo = ldF;
-    if (!pre) g.mt_max = norm_mt("DNN_HIP_GU_MT", M, false);
+    if (!pre) g.mt_max = mp.gu;
     g.ks = pre ? 1 : pick_ks((2 * m->F + 15) / 16, ldD, M, true, g.mt_max);
     g.part = e->part; g.cnt = e->cnt;
     g.kslot = 5 * l + 3;
@@ -351,7 +380,7 @@ int enqueue_layer(dnn_hip_session *s, int l, const PrefillPlan *pp) {
     g.A = e->ACT; g.lda = ldF; g.M = M;
     g.bias = W.f(lo.bd);
     g.out = e->X; g.ldo = ldD; g.res = e->X1; g.ldr = ldD;
-    if (!pre) g.mt_max = plain_mt("DNN_HIP_DOWN_MT", 1);
+    if (!pre) g.mt_max = mp.down;
     g.ks = pre ? 1 : pick_ks((D + 15) / 16, ldF, M, false, g.mt_max);
     g.part = e->part; g.cnt = e->cnt; g.kslot = 5 * l + 4;
     g.pk = !pre;
@@ -380,7 +409,7 @@ int enqueue_head(dnn_hip_session *s, const PrefillPlan *pp, float *logits, int *
     g.prefill = pp != nullptr;
     g.pk = pp == nullptr;                    // decode steps: X in fragment order
     g.kslot = 5 * m->L;
-    if (!pp) g.mt_max = plain_mt("DNN_HIP_HEAD_MT", 0);
+    g.mt_max = mt_plan(g.M, pp == nullptr).head;
     g.ks = pick_ks((m->V + 15) / 16, m->ldD, g.M, true, g.mt_max);
     g.amax_tiles = (m->V + 15) / 16;
     g.part = e->part; g.cnt = e->cnt;

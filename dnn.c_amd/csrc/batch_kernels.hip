@@ -337,7 +337,7 @@ __global__ __launch_bounds__(64 * WM * WN * KW) void gemm_kernel(const GemmArgs 
     // sums of squares), the last to arrive sums all partials in workgroup
     // order (a fixed order: the result does not depend on which one arrives last)
     const size_t n_main = (size_t)g.ks * g.M * g.N;
-    const rsrc_t rp = buf(g.part, g.part ? (n_main + (size_t)gridDim.x * g.M) * 8 : 0);
+    const rsrc_t rp = buf(g.part, g.part ? min(n_main + (size_t)gridDim.x * g.M, g.part_cap) * 8 : 0);
     if (g.ks > 1) {
         for (int i = tid; i < BM * BN / 2; i += GT) {
             const int m = i / (BN / 2), n = 2 * (i - m * (BN / 2));
@@ -1016,6 +1016,12 @@ hipError_t gemm_decode(const GemmArgs &g, hipStream_t st) {
     const int kpw = nks / (kw * g.ks);
     int mt = (g.M + 15) / 16;
     if (g.mt_max > 0 && mt > g.mt_max) mt = g.mt_max;     // row tiles per workgroup (the rest: more workgroups)
+    if (g.ks > 1) {
+        // the split's partials and last-arriver counters must fit their buffers
+        const size_t ntn = (size_t)(g.N + 15) / 16, groups = (size_t)(g.M + 16 * mt - 1) / (16 * mt);
+        const size_t need = (size_t)g.ks * g.M * g.N + ntn * g.ks * g.M;
+        if (!g.part || need > g.part_cap || groups * ntn > (size_t)g.cnt_cap) return hipErrorInvalidValue;
+    }
     switch (mt) {
         case 1: return gemm_decode_mt<EPI, NORM, BF, 1>(g, st, kw, kpw);
         case 2: return gemm_decode_mt<EPI, NORM, BF, 2>(g, st, kw, kpw);

@@ -109,95 +109,6 @@ inline size_t lds_bytes(int nb, int ldD, int ldF) {
     return (size_t)4 * ((LDS_HEAD_WORDS + 3) / 4 * 4) + (size_t)4 * nb * (3 * (size_t)ldD + ldF);
 }
 
-// The lookahead kernel (one or two rows): LDS head, then XS, AS, X1S [nb][ldD],
-// ACTS [nb][ldF], the 2L+1 RMSNorm gammas [ldD], their epsilons, the layer
-// offset table and the RoPE entries of the A units.
-constexpr int LDS4_HEAD_WORDS = (3 * MAXB + 2 * WPB * MAXB + WPB * (DK + 2) + 3 * WPB * 2 * MAXB + 3 * DK +
-                                 WPB * 3 * MAXB * 2 + 3) / 4 * 4;
-inline size_t lds4_bytes(int nb, int ldD, int ldF, int L) {
-    return (size_t)4 * LDS4_HEAD_WORDS + (size_t)4 * nb * (3 * (size_t)ldD + ldF) + (size_t)4 * (2 * L + 1) * ldD +
-           (size_t)4 * (2 * L + 1) + sizeof(LayerOff) * (size_t)L;
-}
-
-// ---- the streaming kernel (one or two rows) --------------------------------
-// Workgroups 0 .. NG-1 run the GEMV phases (wavefront 0 streams weights,
-// wavefronts 1-6 compute, wavefront 7 stages), the last B*H*NS run attention,
-// NS workgroups per (row, head), each over every NS-th 32-key chunk.
-constexpr int S_NCW = WPB - 2;    // compute wavefronts per GEMV workgroup
-constexpr int S_SLOT = 1024;      // weight ring slot: one dwordx4 LDS DMA (64 lanes x 16 B)
-constexpr int S_BSLOT = 256;      // bias slot: one dword LDS DMA (a phase's biases)
-constexpr int S_NBIAS = 8;        // phases in flight (bias slots)
-constexpr int S_MAXREC = 64;      // attention partial records per layer (rows * heads * splits)
-inline int stream_splits(int nb) { return nb == 1 ? 4 : 2; }
-
-// Exchange arena of the streaming kernel (tagged pairs), per layer:
-//   QKV [B][3D] (after bias and RoPE), X1 [B][D], ACT [B][F], X2 [B][D],
-//   AO [B*H*NS][64] unnormalised attention partials (sum_j e^(s_j - m) v_j),
-//   AML [B*H*NS][2] their (m, sum_j e^(s_j - m));
-// then AMAX [2][B][NG][2] (value, index) lm_head argmax partials, double
-// buffered by step parity.
-struct Exch5 {
-    int D, F, B, H, NS, NG;
-    __host__ __device__ size_t nrec() const { return (size_t)B * H * NS; }
-    __host__ __device__ size_t per_layer() const { return (size_t)B * (5 * (size_t)D + F) + nrec() * 66; }
-    __host__ __device__ size_t qkv(int l, int b) const { return per_layer() * l + (size_t)b * 3 * D; }
-    __host__ __device__ size_t x1(int l, int b) const { return per_layer() * l + (size_t)B * 3 * D + (size_t)b * D; }
-    __host__ __device__ size_t act(int l, int b) const { return per_layer() * l + (size_t)B * 4 * D + (size_t)b * F; }
-    __host__ __device__ size_t x2(int l, int b) const {
-        return per_layer() * l + (size_t)B * (4 * (size_t)D + F) + (size_t)b * D;
-    }
-    __host__ __device__ size_t ao(int l) const { return per_layer() * l + (size_t)B * (5 * (size_t)D + F); }
-    __host__ __device__ size_t aml(int l) const { return ao(l) + nrec() * 64; }
-    __host__ __device__ size_t amax(int L, int par, int b, int g) const {
-        return per_layer() * L + (((size_t)par * B + b) * NG + g) * 2;
-    }
-    __host__ __device__ size_t total(int L) const { return per_layer() * L + (size_t)2 * B * NG * 2; }
-};
-
-// LDS of the streaming kernel, byte offsets.  head: ints tok[8] pos[8] done[8]
-// misc[8], the phase table [5][8], the ring slot where each phase in flight
-// starts [S_NBIAS] and its last DMA's issue count [S_NBIAS]; then the RoPE
-// entries of this step [nb][64], the layer table, attention merge partials
-// [WPB][DK+2], the per-wavefront argmax [S_NCW][MAXB][2], the output blocks
-// [2][sout], the staged rows XS, X1S [nb][ldD], then YS, AS [nb][ldD] sharing
-// their space with ACTS [nb][ldF] (the down projection's input is staged after
-// the last read of YS and AS in a layer, and YS is staged again after the
-// down projection), the bias slots [S_NBIAS] and the weight ring [rs] slots.
-struct Lds5 {
-    int rope, lt, part, best, out, xs, ys, as, x1s, acts, ring, bias, total;
-    int rs, sout;
-};
-inline __host__ __device__ Lds5 lds5_layout(int nb, int ldD, int ldF, int L, int sout, int rs) {
-    Lds5 o{};
-    int p = 4 * (32 + 40 + 2 * S_NBIAS);
-    auto take = [&](int bytes) { int r = p; p += (bytes + 15) / 16 * 16; return r; };
-    o.rope = take(4 * nb * 64);
-    o.lt = take((int)sizeof(LayerOff) * L);
-    o.part = take(4 * WPB * (DK + 2));
-    o.best = take(4 * S_NCW * MAXB * 2);
-    o.out = take(4 * 2 * sout);
-    o.xs = take(4 * nb * ldD);
-    o.x1s = take(4 * nb * ldD);
-    o.ys = take(4 * nb * (2 * ldD > ldF ? 2 * ldD : ldF));
-    o.as = o.ys + 4 * nb * ldD;
-    o.acts = o.ys;
-    o.bias = take(S_NBIAS * S_BSLOT);
-    o.ring = take(rs * S_SLOT);
-    o.total = p;
-    o.rs = rs;
-    o.sout = sout;
-    return o;
-}
-
-struct StreamArgs {
-    DecodeArgs a;
-    Exch5 ex;
-    Lds5 lds;
-    int ng;                 // GEMV workgroups; the rest of the grid runs attention
-};
-
 const void *decode_kernel_for(int nb, int dc);
-const void *decode_lookahead_for(int nb, int dc);
-const void *decode_stream_for(int nb, int dc);
 
 }  // namespace dnnhip

@@ -156,39 +156,6 @@ void free_session_buffers(dnn_hip_session *s) {
 
 int pick_nb(int B) { return B > 4 ? 8 : B > 2 ? 4 : B > 1 ? 2 : 1; }
 
-// The streaming kernel's launch shape for this model, batch and grid, or
-// false where it does not apply (the general kernel runs instead): every GEMV
-// workgroup must own out_proj and down rows (so each takes part in every
-// layer), a workgroup's biases of a phase must fit one 64-lane gather (32
-// gate + 32 up for gate/up), the attention partials one 64-lane merge, and
-// the weight ring must hold any one phase of a workgroup.
-bool stream_plan(const dnn_hip_model *m, int B, int grid, int lds_max, StreamArgs *sa) {
-    if (B > 2) return false;
-    const int nb = B, NS = stream_splits(nb), NA = B * m->H * NS, NG = grid - NA;
-    if (NG < 1 || NG > m->D || NA > S_MAXREC) return false;
-    const int DC = m->ldD / LDALIGN, FC = m->ldF / LDALIGN;
-    const int nu[5] = {3 * m->D / 2, m->D, m->F, m->D, m->V};
-    const int R[5] = {2, 1, 2, 1, 1};
-    const int ch[5] = {DC, DC, DC, FC, DC};
-    const int bias_cap[5] = {WAVE / 2, WAVE, WAVE / 2, WAVE, WAVE};
-    const int out_per_unit[4] = {2, 1, 1, 1};
-    int sout = 0, ring_need = 0;
-    for (int k = 0; k < 5; k++) {
-        const int n_wg = (nu[k] + NG - 1) / NG;
-        if (n_wg > bias_cap[k]) return false;
-        ring_need = std::max(ring_need, n_wg * R[k] * ch[k]);
-        if (k < 4) sout = std::max(sout, nb * n_wg * out_per_unit[k]);
-    }
-    const int fixed = lds5_layout(nb, m->ldD, m->ldF, m->L, sout, 0).total;
-    const int rs = (lds_max - fixed) / S_SLOT;
-    if (rs < ring_need) return false;
-    sa->lds = lds5_layout(nb, m->ldD, m->ldF, m->L, sout, rs);
-    if (sa->lds.total > lds_max) return false;
-    sa->ex = Exch5{m->D, m->F, B, m->H, NS, NG};
-    sa->ng = NG;
-    return true;
-}
-
 }  // namespace
 
 extern "C" {
@@ -327,10 +294,9 @@ int dnn_hip_session_create(dnn_hip_model *m, int B, int max_seq, dnn_hip_session
     // the batched engine for more than 4 rows (from 5 rows on it beats the
     // persistent kernel, which runs 5-8 rows at its 8-row cost: C2 at 8 rows
     // 17.8k vs 15.4k tokens/s, 1,024-key histories 14.5k vs 11.5k), bf16
-    // weights, or on request; DNN_HIP_DECODE_KERNEL=3/4/5 keeps up to 8 rows
-    // on the persistent kernels
-    const bool persistent_pref = s->kernel_pref >= 3 && s->kernel_pref <= 5;
-    s->batched = B > MAXB || m->bf16 || s->kernel_pref == 6 || (B > 4 && !persistent_pref);
+    // weights, or on request; DNN_HIP_DECODE_KERNEL=3 keeps up to 8 rows on
+    // the persistent kernel
+    s->batched = B > MAXB || m->bf16 || s->kernel_pref == 6 || (B > 4 && s->kernel_pref != 3);
     int n_cu = 0;
     if (hipDeviceGetAttribute(&n_cu, hipDeviceAttributeMultiprocessorCount, m->device) != hipSuccess || n_cu <= 0) n_cu = 256;
     s->grid_cap = n_cu;
@@ -338,13 +304,7 @@ int dnn_hip_session_create(dnn_hip_model *m, int B, int max_seq, dnn_hip_session
     s->ex = Exch{m->ldD, m->ldF, m->D, B, s->grid_cap, m->H, B * m->H <= ATT_SPLIT_HEADS ? ATT_SPLIT_MAX : 1};
     // the kernels read whole 64-key chunks: the row stride kv_s covers them
     const size_t kv = (size_t)m->L * B * m->H * s->kv_s * DK + (size_t)CH * DK;
-    size_t xa_pairs = s->batched ? 1 : s->ex.total(m->L);
-    if (!s->batched && B <= 2) {
-        // room for the streaming kernel's exchange layout (its grid <= grid_cap)
-        const int nb = pick_nb(B);
-        const Exch5 e5{m->D, m->F, B, m->H, stream_splits(nb), s->grid_cap};
-        xa_pairs = std::max(xa_pairs, e5.total(m->L));
-    }
+    const size_t xa_pairs = s->batched ? 1 : s->ex.total(m->L);
     s->xa_pairs = xa_pairs;
     if (kv * sizeof(float) >= 0x7fffffffu || xa_pairs * 8 >= 0x7fffffffu) {
         delete s;
@@ -502,31 +462,10 @@ int decode_launch(dnn_hip_session *s, const int *feed, int n_feed_all, const int
     HIP_TRY(hipDeviceGetAttribute(&lds_max, hipDeviceAttributeMaxSharedMemoryPerBlock, m->device));
     int grid = s->grid_cap;
     if (s->grid_req > 0) grid = std::min(grid, s->grid_req);
-    // decode_v3 by default; the lookahead kernel (one or two rows) on request,
-    // when its schedule fits (every GEMV round in at most 3 slots of the grid's
-    // non-attention workgroups) and its LDS does.
-    const void *kern = nullptr;
-    size_t shmem = 0;
-    StreamArgs sa{};
-    bool stream = false;
-    if (s->kernel_pref == 5 && stream_plan(m, B, grid, lds_max, &sa) &&
-        sa.ex.total(m->L) <= s->xa_pairs) {
-        kern = decode_stream_for(nb, dc);
-        shmem = (size_t)sa.lds.total;
-        stream = kern != nullptr;
-    }
-    const int rounds = (m->D + 6) / 7 + (3 * m->D / 2 + 6) / 7 + (m->D / 2 + 6) / 7 + (m->F + 6) / 7;
-    if (!kern && nb <= 2 && s->kernel_pref == 4 && grid > B * m->H && rounds <= 3 * (grid - B * m->H) &&
-        lds4_bytes(nb, m->ldD, m->ldF, m->L) <= (size_t)lds_max) {
-        kern = decode_lookahead_for(nb, dc);
-        shmem = lds4_bytes(nb, m->ldD, m->ldF, m->L);
-    }
-    if (!kern) {
-        kern = decode_kernel_for(nb, dc);
-        shmem = lds_bytes(nb, m->ldD, m->ldF);
-    }
+    const void *kern = decode_kernel_for(nb, dc);
+    const size_t shmem = lds_bytes(nb, m->ldD, m->ldF);
     if (!kern) return fail(DNN_HIP_EINVAL, "d_model %d: the decode kernels cover d_model <= %d", m->D, 3 * LDALIGN);
-    s->kernel_used = stream ? 5 : kern == decode_kernel_for(nb, dc) ? 3 : 4;
+    s->kernel_used = 3;
     rc = grow(&s->feed, &s->feed_cap, (size_t)nf_max * B);
     if (!rc) rc = grow(&s->ids, &s->ids_cap, (size_t)n_steps * B);
     if (!rc && want_logits) rc = grow(&s->logits, &s->logits_cap, (size_t)n_steps * B * m->V);
@@ -561,14 +500,13 @@ int decode_launch(dnn_hip_session *s, const int *feed, int n_feed_all, const int
     a.B = B; a.max_seq = s->kv_s;
     a.kc = s->kc; a.vc = s->vc; a.xa = s->xa; a.ex = s->ex;
     a.ex.grid = s->grid_cap;
-    a.ex.ns = s->kernel_used == 3 ? att_splits(s, grid, n_steps) : 1;
+    a.ex.ns = att_splits(s, grid, n_steps);
     s->att_splits = a.ex.ns;
     a.pos = s->pos; a.feed = s->feed; a.n_feed = s->n_feed;
     a.ids = s->ids; a.logits = want_logits ? s->logits : nullptr;
     a.n_steps = n_steps; a.eos = eos; a.step0 = s->next_tag; a.err = s->err; a.steps_done = s->steps_done;
     s->next_tag += (unsigned)n_steps;
-    sa.a = a;
-    void *kargs[] = {stream ? static_cast<void *>(&sa) : static_cast<void *>(&a)};
+    void *kargs[] = {&a};
     HIP_TRY(hipEventRecord(s->ev0, s->stream));
     HIP_TRY(hipLaunchKernel(kern, dim3(grid), dim3(BLOCK), kargs, shmem, s->stream));
     HIP_TRY(hipEventRecord(s->ev1, s->stream));

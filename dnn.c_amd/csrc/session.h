@@ -85,8 +85,8 @@ struct dnn_hip_session {
     size_t logits_cap = 0;
     int grid_req = 0, grid = 0, grid_cap = 0;
     unsigned next_tag = 1;                    // tags only grow: stale values never match
-    int kernel_pref = 0;                      // env DNN_HIP_DECODE_KERNEL: 4 / 5 / 6: lookahead / streaming / batched engine
-    int kernel_used = 0;                      // 3, 4, 5 or 6: the kernel of the last launch
+    int kernel_pref = 0;                      // env DNN_HIP_DECODE_KERNEL: 3 persistent kernel (up to 8 rows) / 6 batched engine
+    int kernel_used = 0;                      // 3 or 6: the kernel of the last launch
     int att_splits_req = 0;                   // env DNN_HIP_ATT_SPLITS: workgroups per head in decode_v3 (0 = auto)
     int att_splits = 1;                       // the last decode_v3 launch's
     size_t xa_pairs = 0;

@@ -3,7 +3,7 @@
  * The decoder_lm struct is the reference's and has no room for a device
  * handle, so mirrors live in a small table keyed by the model pointer.  A
  * mirror is refreshed when a fingerprint of the host parameters changes: the
- * parameter pointers and shapes, 64 evenly spaced values of every tensor, and
+ * parameter pointers and shapes, 4,096 evenly spaced values of every tensor, and
  * the RoPE table pointers.  Training or module_load rewrite whole tensors and
  * change it; decoder_lm_device_sync covers edits the samples could miss. */
 #include "device.h"
@@ -35,19 +35,41 @@ static uint64_t mix(uint64_t h, uint64_t v) {
     return h * 1099511628211ULL;
 }
 
+/* Identity of the host weights the HBM mirror was made from: every
+ * parameter's pointer and size plus 4,096 evenly spaced values of it (about a
+ * millisecond for the C2 model).  An in-place edit that touches none of the
+ * sampled elements is not seen: such callers call decoder_lm_device_sync, or
+ * set DNN_AMD_SYNC=full, which checksums every value (a position-weighted sum,
+ * about 80 ms for the C2 model's 365 MB) before each device call. */
 static uint64_t fingerprint(decoder_lm *lm) {
+    static int full = -1;
+    if (full < 0) {
+        const char *e = getenv("DNN_AMD_SYNC");
+        full = e && strcmp(e, "full") == 0;
+    }
     int n;
     tensor **ps = module_parameters(&lm->base, &n);
     uint64_t h = 1469598103934665603ULL;
     for (int i = 0; i < n; i++) {
-        const int ne = tensor_numel(ps[i]);
+        const long long ne = tensor_numel(ps[i]);
         const float *d = tensor_data_ptr(ps[i]);
         h = mix(h, (uint64_t)(uintptr_t)d);
         h = mix(h, (uint64_t)ne);
-        for (int k = 0; k < 64; k++) {
-            uint32_t bits;
-            memcpy(&bits, &d[(long long)k * ne / 64], 4);
-            h = mix(h, bits);
+        if (full) {
+            uint64_t a = 0, b = 0;
+            const uint32_t *w = (const uint32_t *)d;
+            for (long long k = 0; k < ne; k++) {
+                a += w[k];
+                b += (uint64_t)w[k] * (uint64_t)(uint32_t)(k + 1);
+            }
+            h = mix(mix(h, a), b);
+        } else {
+            const int ns = ne < 4096 ? (int)ne : 4096;
+            for (int k = 0; k < ns; k++) {
+                uint32_t bits;
+                memcpy(&bits, &d[(long long)k * ne / ns], 4);
+                h = mix(h, bits);
+            }
         }
     }
     tensor *fc = lm->blocks[0]->freqs_cos;

@@ -176,8 +176,13 @@ void module_load(module *m, const char *path, int strict) {
     size_t r = fread(magic, 1, 4, f);
     assert(r == 4 && memcmp(magic, "DNNM", 4) == 0 && "module_load: bad magic");
     (void)r;
-    assert(get_u32(f) == 1 && "module_load: unsupported version");
-    assert(get_u32(f) == 16 && "module_load: unexpected header size");
+    /* read into locals first: the asserts must not hold the reads (-DNDEBUG) */
+    const uint32_t version = get_u32(f);
+    const uint32_t header_size = get_u32(f);
+    assert(version == 1 && "module_load: unsupported version");
+    assert(header_size == 16 && "module_load: unexpected header size");
+    (void)version;
+    (void)header_size;
     uint32_t entries = get_u32(f);
     char name[MODULE_STATE_MAX_NAME] = "";
     int live = 0;

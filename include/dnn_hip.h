@@ -196,17 +196,14 @@ int dnn_hip_session_last_ms(dnn_hip_session *s, float *ms);
 int dnn_hip_session_set_grid(dnn_hip_session *s, int n_workgroups);
 /* Workgroups the last dnn_hip_decode launch on this session used. */
 int dnn_hip_session_grid(dnn_hip_session *s, int *n_workgroups);
-/* Which decode kernel the last dnn_hip_decode launch used: 3 = the general
- * persistent one (up to 4 rows by default, up to 8 when
- * DNN_HIP_DECODE_KERNEL=3), 4 = the layer-lookahead kernel, 5 = the streaming
- * kernel (both 1-2 rows), chosen when the environment variable
- * DNN_HIP_DECODE_KERNEL is 4 or 5 at session creation and the kernel's
- * schedule fits the model and grid; 6 = the batched engine (more rows, bf16
- * weights, or DNN_HIP_DECODE_KERNEL=6). */
+/* Which decode path the last dnn_hip_decode call used: 3 = the persistent
+ * kernel (up to 4 rows by default, up to 8 when DNN_HIP_DECODE_KERNEL=3 at
+ * session creation), 6 = the batched engine (more rows, bf16 weights, or
+ * DNN_HIP_DECODE_KERNEL=6). */
 int dnn_hip_session_kernel(dnn_hip_session *s, int *which);
 /* Workgroups per (row, head) over which the last decode call split each
- * head's cached keys, on the general kernel (3) or the batched engine (6); 1 on
- * the other kernels (1 = unsplit; chosen from the call's longest history, or
+ * head's cached keys, on the persistent kernel (3) or the batched engine (6); 1 on
+ * the other paths (1 = unsplit; chosen from the call's longest history, or
  * fixed by the environment variable DNN_HIP_ATT_SPLITS at session creation). */
 int dnn_hip_session_att_splits(dnn_hip_session *s, int *splits);
 

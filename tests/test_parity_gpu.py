@@ -126,67 +126,6 @@ def test_batch_rows_match_independent_runs(c1g, monkeypatch, B, kern):
     assert s.kernel() == (3 if B <= 4 or kern == "3" else 6)
 
 
-@pytest.mark.parametrize("B", [1, 2])
-def test_lookahead_kernel_equals_general_kernel(golden, c2, monkeypatch, B):
-    """The layer-lookahead kernel (one or two rows, on request): its tokens equal
-    the general kernel's and its logits agree within the parity bar (its
-    attention sums the query-key products in another order)."""
-    _, hm = c2
-    toks = np.array(golden["c2_tokens"][:48], dtype=np.int32)
-    feed = np.stack([toks] * B, axis=1) if B > 1 else toks
-    monkeypatch.setenv("DNN_HIP_DECODE_KERNEL", "3")
-    s3 = A.HipSession(hm, B, 64)
-    ids3, lg3 = s3.decode(feed, 48, want_logits=True)
-    assert s3.kernel() == 3
-    monkeypatch.setenv("DNN_HIP_DECODE_KERNEL", "4")
-    s4 = A.HipSession(hm, B, 64)
-    ids4, lg4 = s4.decode(feed, 48, want_logits=True)
-    assert s4.kernel() == 4
-    assert np.array_equal(ids4, ids3)
-    for b in range(B):
-        assert_logits_close(lg4[:, b], lg3[:, b], "row %d" % b)
-
-
-@pytest.mark.parametrize("B", [1, 2])
-def test_streaming_kernel_matches_general_kernel(golden, c2, monkeypatch, B):
-    """The streaming kernel (one or two rows, on request): its tokens equal
-    the general kernel's and its logits agree within the parity bar (the
-    attention splits merge in a different order)."""
-    _, hm = c2
-    toks = np.array(golden["c2_tokens"][:48], dtype=np.int32)
-    feed = np.stack([toks] * B, axis=1) if B > 1 else toks
-    monkeypatch.setenv("DNN_HIP_DECODE_KERNEL", "5")
-    s5 = A.HipSession(hm, B, 64)
-    ids5, lg5 = s5.decode(feed, 48, want_logits=True)
-    assert s5.kernel() == 5
-    monkeypatch.setenv("DNN_HIP_DECODE_KERNEL", "3")
-    s3 = A.HipSession(hm, B, 64)
-    ids3, lg3 = s3.decode(feed, 48, want_logits=True)
-    assert s3.kernel() == 3
-    assert np.array_equal(ids5, ids3)
-    for b in range(B):
-        assert_logits_close(lg5[:, b], lg3[:, b], "row %d" % b)
-
-
-@pytest.mark.parametrize("B,steps", [(1, 1100), (2, 600)])
-def test_streaming_kernel_long_history(monkeypatch, B, steps):
-    """Histories longer than one 32-key chunk per attention wavefront (1024
-    keys with 4 splits per head, 512 with 2): the wavefronts walk several
-    chunks.  Every row's tokens and logits against the oracle."""
-    m = O.Model(128, 256, 4, 4, 683, steps + 8, seed=11, init="gpt2")
-    hm = hip_model(m)
-    rng = np.random.default_rng(steps)
-    feed = rng.integers(0, 128, size=(4, B)).astype(np.int32)
-    monkeypatch.setenv("DNN_HIP_DECODE_KERNEL", "5")
-    s = A.HipSession(hm, B, steps + 8)
-    ids, lg = s.decode(feed, steps, n_feed=np.full(B, 4, np.int32), want_logits=True)
-    assert s.kernel() == 5
-    for b in range(B):
-        want, wlg = m.generate(feed[:, b], steps - 3, eos=-1, want_logits=True)
-        assert list(ids[3:, b]) == list(want[4:]), "row %d" % b
-        assert_logits_close(lg[3:, b], wlg, "row %d" % b)
-
-
 @pytest.mark.parametrize("B,splits", [(1, 2), (1, 3), (1, 4), (2, 4), (8, 4)])
 def test_general_kernel_split_attention(monkeypatch, B, splits):
     """The general kernel with each head's keys split over several workgroups
