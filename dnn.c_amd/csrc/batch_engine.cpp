@@ -448,8 +448,13 @@ int engine_decode(dnn_hip_session *s, const int *feed, int n_feed_all, const int
     if (!rc && logits) rc = grow(&s->logits, &s->logits_cap, (size_t)n_steps * B * m->V);
     if (rc) return rc;
     BatchEngine *e = s->eng;
-    HIP_TRY(hipMemcpyAsync(s->feed, feed, sizeof(int) * (size_t)nf_max * B, hipMemcpyHostToDevice, s->stream));
-    HIP_TRY(hipMemcpyAsync(s->n_feed, nf.data(), sizeof(int) * B, hipMemcpyHostToDevice, s->stream));
+    {
+        const size_t feed_bytes = sizeof(int) * (size_t)nf_max * B, nf_bytes = sizeof(int) * B;
+        rc = stage_begin(s, stage_size(feed_bytes) + stage_size(nf_bytes));
+        if (!rc) rc = stage_copy(s, s->feed, feed, feed_bytes);
+        if (!rc) rc = stage_copy(s, s->n_feed, nf.data(), nf_bytes);
+        if (rc) return rc;
+    }
 
     // the decode attention's speculative loads: the leading wavefronts whose
     // first chunk (64 keys of split 0) at least 3/4 of this call's (row, step)
@@ -573,15 +578,19 @@ int engine_prefill(dnn_hip_session *s, const float *embeds, int n_embed, const i
     std::copy(tiles.begin(), tiles.end(), htiles);
     rc = grow(&e->pre_i, &e->pre_cap, plan.size());
     if (rc) return rc;
-    HIP_TRY(hipMemcpyAsync(e->pre_i, plan.data(), plan.size() * sizeof(int), hipMemcpyHostToDevice, s->stream));
+    const size_t emb_row = (size_t)D * 4 * n_embed;
+    rc = stage_begin(s, stage_size(plan.size() * sizeof(int)) + (size_t)B * stage_size(emb_row));
+    if (!rc) rc = stage_copy(s, e->pre_i, plan.data(), plan.size() * sizeof(int));
+    if (rc) return rc;
     int *d = e->pre_i;
     PrefillPlan pp{M, d, d + M, d + 2 * M, d + 3 * M, d + 3 * M + B, d + 3 * M + 2 * B, d + 3 * M + 3 * B,
                    d + 3 * M + 4 * B, T, mode, prefix_len};
     // embedding inputs (e.g. image patches) straight into their rows, token rows gathered
     if (n_embed > 0)
-        for (int b = 0; b < B; b++)
-            HIP_TRY(hipMemcpy2DAsync(e->X + (size_t)row0[b] * m->ldD, (size_t)m->ldD * 4, embeds + (size_t)b * n_embed * D,
-                                     (size_t)D * 4, (size_t)D * 4, n_embed, hipMemcpyHostToDevice, s->stream));
+        for (int b = 0; b < B && !rc; b++)
+            rc = stage_copy2d(s, e->X + (size_t)row0[b] * m->ldD, (size_t)m->ldD * 4, embeds + (size_t)b * n_embed * D,
+                              (size_t)D * 4, (size_t)D * 4, n_embed);
+    if (rc) return rc;
     EmbedArgs ea{};
     ea.embed = reinterpret_cast<const float *>(m->arena) + m->off.embed / 4;
     ea.ids = pp.pid; ea.out = e->X; ea.M = M; ea.ld = m->ldD; ea.D = D;
@@ -640,11 +649,13 @@ int engine_block(dnn_hip_session *s, int layer, const float *x, int n_new, int p
     std::copy(tiles.begin(), tiles.end(), htiles);
     rc = grow(&e->pre_i, &e->pre_cap, plan.size());
     if (rc) return rc;
-    HIP_TRY(hipMemcpyAsync(e->pre_i, plan.data(), plan.size() * sizeof(int), hipMemcpyHostToDevice, s->stream));
+    rc = stage_begin(s, stage_size(plan.size() * sizeof(int)) + stage_size((size_t)D * 4 * M));
+    if (!rc) rc = stage_copy(s, e->pre_i, plan.data(), plan.size() * sizeof(int));
+    if (!rc) rc = stage_copy2d(s, e->X, (size_t)m->ldD * 4, x, (size_t)D * 4, (size_t)D * 4, M);
+    if (rc) return rc;
     int *d = e->pre_i;
     PrefillPlan pp{M, d, d + M, d + 2 * M, d + 3 * M, d + 3 * M + B, d + 3 * M + 2 * B, d + 3 * M + 3 * B,
                    d + 3 * M + 4 * B, T, mode, prefix_len};
-    HIP_TRY(hipMemcpy2DAsync(e->X, (size_t)m->ldD * 4, x, (size_t)D * 4, (size_t)D * 4, M, hipMemcpyHostToDevice, s->stream));
     HIP_TRY(hipEventRecord(s->ev0, s->stream));
     rc = enqueue_layer(s, layer, &pp);
     if (rc) return rc;
@@ -669,8 +680,10 @@ int engine_head(dnn_hip_session *s, const float *x, int n, int norm, float *logi
     for (int i = 0; i < n; i++) rows[i] = i;
     rc = grow(&e->pre_i, &e->pre_cap, (size_t)n);
     if (rc) return rc;
-    HIP_TRY(hipMemcpyAsync(e->pre_i, rows.data(), (size_t)n * sizeof(int), hipMemcpyHostToDevice, s->stream));
-    HIP_TRY(hipMemcpy2DAsync(e->X, (size_t)m->ldD * 4, x, (size_t)D * 4, (size_t)D * 4, n, hipMemcpyHostToDevice, s->stream));
+    rc = stage_begin(s, stage_size((size_t)n * sizeof(int)) + stage_size((size_t)D * 4 * n));
+    if (!rc) rc = stage_copy(s, e->pre_i, rows.data(), (size_t)n * sizeof(int));
+    if (!rc) rc = stage_copy2d(s, e->X, (size_t)m->ldD * 4, x, (size_t)D * 4, (size_t)D * 4, n);
+    if (rc) return rc;
     for (int r0 = 0; r0 < n; r0 += BK_MAXM) {
         const int cnt = std::min(BK_MAXM, n - r0);
         PrefillPlan pp{};
@@ -696,7 +709,9 @@ int engine_embed(dnn_hip_session *s, const int *ids, int n, float *out) {
     BatchEngine *e = s->eng;
     rc = grow(&e->pre_i, &e->pre_cap, (size_t)n);
     if (rc) return rc;
-    HIP_TRY(hipMemcpyAsync(e->pre_i, ids, (size_t)n * sizeof(int), hipMemcpyHostToDevice, s->stream));
+    rc = stage_begin(s, stage_size((size_t)n * sizeof(int)));
+    if (!rc) rc = stage_copy(s, e->pre_i, ids, (size_t)n * sizeof(int));
+    if (rc) return rc;
     EmbedArgs ea{};
     ea.embed = reinterpret_cast<const float *>(m->arena) + m->off.embed / 4;
     ea.ids = e->pre_i; ea.out = e->X; ea.M = n; ea.ld = m->ldD; ea.D = m->D;
@@ -716,8 +731,10 @@ int engine_rms_norm(dnn_hip_session *s, const float *x, const float *gamma, int 
     if (rc) return rc;
     BatchEngine *e = s->eng;
     float *g = e->X1;                                  // gamma in row 0 of X1, rows of x in X, y into ATT
-    HIP_TRY(hipMemcpyAsync(g, gamma, sizeof(float) * d, hipMemcpyHostToDevice, s->stream));
-    HIP_TRY(hipMemcpy2DAsync(e->X, (size_t)m->ldD * 4, x, (size_t)d * 4, (size_t)d * 4, n, hipMemcpyHostToDevice, s->stream));
+    rc = stage_begin(s, stage_size(sizeof(float) * d) + stage_size((size_t)d * 4 * n));
+    if (!rc) rc = stage_copy(s, g, gamma, sizeof(float) * d);
+    if (!rc) rc = stage_copy2d(s, e->X, (size_t)m->ldD * 4, x, (size_t)d * 4, (size_t)d * 4, n);
+    if (rc) return rc;
     HIP_TRY(launch_rms_rows(e->X, g, e->ATT, n, d, m->ldD, eps, s->stream));
     HIP_TRY(hipMemcpy2DAsync(y, (size_t)d * 4, e->ATT, (size_t)m->ldD * 4, (size_t)d * 4, n, hipMemcpyDeviceToHost, s->stream));
     HIP_TRY(hipStreamSynchronize(s->stream));

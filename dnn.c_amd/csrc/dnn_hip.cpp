@@ -361,6 +361,7 @@ int dnn_hip_session_destroy(dnn_hip_session *s) {
     if (s->ev0) (void)hipEventDestroy(s->ev0);
     if (s->ev1) (void)hipEventDestroy(s->ev1);
     if (s->stream) (void)hipStreamDestroy(s->stream);
+    if (s->stage) (void)hipHostFree(s->stage);
     delete s;
     return DNN_HIP_OK;
 }
@@ -396,6 +397,47 @@ int dnn_hip_session_last_ms(dnn_hip_session *s, float *ms) {
 }
 
 extern "C++" {
+int dnnhip::stage_begin(dnn_hip_session *s, size_t bytes) {
+    s->stage_used = 0;
+    if (bytes <= s->stage_cap) return DNN_HIP_OK;
+    HIP_TRY(hipStreamSynchronize(s->stream));
+    if (s->stage) (void)hipHostFree(s->stage);
+    s->stage = nullptr;
+    s->stage_cap = 0;
+    const size_t cap = std::max(bytes, (size_t)64 << 10);
+    const hipError_t e = hipHostMalloc(reinterpret_cast<void **>(&s->stage), cap, hipHostMallocDefault);
+    if (e != hipSuccess) {
+        s->stage = nullptr;
+        return fail(DNN_HIP_ENOMEM, "hipHostMalloc(%zu) for the staging buffer: %s", cap, hipGetErrorString(e));
+    }
+    s->stage_cap = cap;
+    return DNN_HIP_OK;
+}
+
+int dnnhip::stage_copy(dnn_hip_session *s, void *dst, const void *src, size_t bytes) {
+    if (bytes == 0) return DNN_HIP_OK;
+    if (s->stage_used + stage_size(bytes) > s->stage_cap)
+        return fail(DNN_HIP_EINVAL, "staging: %zu bytes past the %zu reserved", s->stage_used + bytes, s->stage_cap);
+    char *p = s->stage + s->stage_used;
+    memcpy(p, src, bytes);
+    s->stage_used += stage_size(bytes);
+    HIP_TRY(hipMemcpyAsync(dst, p, bytes, hipMemcpyHostToDevice, s->stream));
+    return DNN_HIP_OK;
+}
+
+int dnnhip::stage_copy2d(dnn_hip_session *s, void *dst, size_t dpitch, const void *src, size_t spitch, size_t width,
+                         size_t rows) {
+    if (width == 0 || rows == 0) return DNN_HIP_OK;
+    const size_t bytes = width * rows;
+    if (s->stage_used + stage_size(bytes) > s->stage_cap)
+        return fail(DNN_HIP_EINVAL, "staging: %zu bytes past the %zu reserved", s->stage_used + bytes, s->stage_cap);
+    char *p = s->stage + s->stage_used;
+    for (size_t r = 0; r < rows; r++) memcpy(p + r * width, static_cast<const char *>(src) + r * spitch, width);
+    s->stage_used += stage_size(bytes);
+    HIP_TRY(hipMemcpy2DAsync(dst, dpitch, p, width, width, rows, hipMemcpyHostToDevice, s->stream));
+    return DNN_HIP_OK;
+}
+
 int dnnhip::check_decode(dnn_hip_session *s, const int *feed, int n_feed_all, const int *n_feed, int n_steps,
                          std::vector<int> &nf, int *nf_max) {
     dnn_hip_model *m = s->m;
@@ -470,8 +512,11 @@ int decode_launch(dnn_hip_session *s, const int *feed, int n_feed_all, const int
     if (!rc) rc = grow(&s->ids, &s->ids_cap, (size_t)n_steps * B);
     if (!rc && want_logits) rc = grow(&s->logits, &s->logits_cap, (size_t)n_steps * B * m->V);
     if (rc) return rc;
-    HIP_TRY(hipMemcpyAsync(s->feed, feed, sizeof(int) * (size_t)nf_max * B, hipMemcpyHostToDevice, s->stream));
-    HIP_TRY(hipMemcpyAsync(s->n_feed, nf.data(), sizeof(int) * B, hipMemcpyHostToDevice, s->stream));
+    const size_t feed_bytes = sizeof(int) * (size_t)nf_max * B, nf_bytes = sizeof(int) * B;
+    rc = stage_begin(s, stage_size(feed_bytes) + stage_size(nf_bytes));
+    if (!rc) rc = stage_copy(s, s->feed, feed, feed_bytes);
+    if (!rc) rc = stage_copy(s, s->n_feed, nf.data(), nf_bytes);
+    if (rc) return rc;
     HIP_TRY(hipMemsetAsync(s->err, 0, sizeof(int), s->stream));
 
     // One workgroup (8 wavefronts) per CU: the dataflow waits need every

@@ -91,6 +91,10 @@ struct dnn_hip_session {
     int att_splits = 1;                       // the last decode_v3 launch's
     size_t xa_pairs = 0;
     float last_ms = 0.f;
+    // pinned host staging of one call's host-to-device copies (hipHostMalloc):
+    // every copy into the device is made from here, never from caller memory
+    char *stage = nullptr;
+    size_t stage_cap = 0, stage_used = 0;
     std::vector<int> h_pos;
     BatchEngine *eng = nullptr;
 };
@@ -120,6 +124,18 @@ int grow(T **p, size_t *cap, size_t count) {
     if (rc == DNN_HIP_OK) *cap = count;
     return rc;
 }
+
+// Host-to-device copies of one call go through the session's pinned staging:
+// stage_begin reserves `bytes` (rounded up per copy to 256) and resets the
+// offset; stage_copy / stage_copy2d copy the caller's bytes into the staging
+// buffer and enqueue the asynchronous copy on the session's stream.  Every
+// call that stages synchronises its stream before it returns, so the next
+// call's staging never overwrites a copy still in flight.
+int stage_begin(dnn_hip_session *s, size_t bytes);
+int stage_copy(dnn_hip_session *s, void *dst, const void *src, size_t bytes);
+int stage_copy2d(dnn_hip_session *s, void *dst, size_t dpitch, const void *src, size_t spitch, size_t width,
+                 size_t rows);
+inline size_t stage_size(size_t bytes) { return (bytes + 255) / 256 * 256; }
 
 // argument checks of dnn_hip_decode: nf[b] = feed rows of row b
 int check_decode(dnn_hip_session *s, const int *feed, int n_feed_all, const int *n_feed, int n_steps,
