@@ -30,13 +30,13 @@ CONFIGS = {
     # name: V, D, L, H, F, prompt, batch
     "c1": (128, 256, 4, 4, 683, 16, 1),
     "c2": (8192, 768, 12, 12, 2048, 32, 1),
-    "c3": (8192, 768, 12, 12, 2048, 32, 32),
+    "c3": (8192, 768, 12, 12, 2048, 64, 32),
     "c2b2": (8192, 768, 12, 12, 2048, 32, 2),
     "c2b4": (8192, 768, 12, 12, 2048, 32, 4),
     "c2b8": (8192, 768, 12, 12, 2048, 32, 8),
 }
 SEED = {"c1": 1, "c2": 2, "c3": 3, "c2b2": 2, "c2b4": 2, "c2b8": 2, "c4": 4, "c5": 5}
-KERNELS = {3: "decode_v3<NB,DC>", 4: "decode_v4<NB,DC>", 5: "decode_v5<NB,DC>",
+KERNELS = {3: "decode_v3<NB,DC>",
            6: "batched engine: gemm_kernel / attn_kernel chain, one HIP graph replay per step"}
 
 
@@ -101,46 +101,83 @@ def weight_floats(V, D, Ly, F):
 def step_bytes(V, D, Ly, F, positions, B):
     """Algorithmic HBM bytes of the decode steps whose new tokens sit at
     `positions` (0-based, S = pos+1 cached keys attended): every weight once per
-    step, each row's K and V history read once per layer, one K and V row written."""
+    step, each row's K and V history read once per layer, one K and V row
+    written.  `positions` holds one position per step for B rows at the same
+    position, or (per-row lengths) one list of B positions per step."""
     w = 4 * weight_floats(V, D, Ly, F)
     total = 0
     for p in positions:
-        kv_read = Ly * 2 * (p + 1) * D * 4 * B
-        kv_write = Ly * 2 * D * 4 * B
-        total += w + kv_read + kv_write
+        rows = list(p) if hasattr(p, "__len__") else [p] * B
+        total += w
+        for q in rows:
+            total += Ly * 2 * (q + 1) * D * 4 + Ly * 2 * D * 4
     return total
 
 
 def measured_traffic(cfg, positions):
     """HBM bytes of this launch from the committed rocprofv3 --pmc summary of
-    the same workload (profiles/traffic_<cfg>.json: FETCH_SIZE + WRITE_SIZE
-    per step, scaled by a copy kernel of known size), or None if absent."""
+    the same workload (profiles/traffic_<cfg>.json: FETCH_SIZE + WRITE_SIZE of
+    one launch, scaled by a copy kernel of known size).  Returns (bytes of this
+    launch or None, the profiled launch's record): the bytes only when this
+    launch covers exactly the profiled positions -- a launch over other
+    positions moves other K/V bytes, and no figure is extrapolated."""
     path = os.path.join(ROOT, "profiles", "traffic_%s.json" % cfg)
     if not os.path.exists(path):
-        return None
+        return None, None
     with open(path) as f:
         t = json.load(f)
-    return int(round(t["hbm_bytes_per_step"] * len(positions)))
+    rec = {k: t[k] for k in ("positions", "steps", "hbm_bytes", "algorithmic_bytes", "profile") if k in t}
+    if list(t.get("positions", [])) == [positions[0], positions[-1]]:
+        return int(t["hbm_bytes"]), rec
+    return None, rec
 
 
-def cpu_baseline(cfg, budget_tokens):
-    """The reference itself (oracle/_ref/ref_bench, built from its sources), one
-    thread, on a bounded sample of the same model: 4-token prompt, then
-    `budget_tokens` greedy steps; falls back to the oracle port if absent."""
-    V, D, Ly, H, F, _, _ = CONFIGS[cfg]
+def host_identity():
+    """The CPU the baseline ran on: nproc, the lscpu model name, OMP_NUM_THREADS."""
+    model = ""
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    model = line.split(":", 1)[1].strip()
+                    break
+    except OSError:
+        pass
+    return {"nproc": os.cpu_count(), "cpu_model": model, "OMP_NUM_THREADS": os.environ.get("OMP_NUM_THREADS")}
+
+
+def ref_bench(cfg, prompt, new_tokens, seed=None):
+    """One run of oracle/_ref/ref_bench (the reference built from its own
+    sources, greedy decoder_lm_generate with the KV cache, one thread):
+    returns its JSON record, or None where the reference build is absent."""
+    V, D, Ly, H, F = CONFIGS[cfg][:5]
     exe = os.path.join(ROOT, "oracle", "_ref", "ref_bench")
+    if not os.path.exists(exe):
+        return None
     env = dict(os.environ, OMP_NUM_THREADS="1")
-    sample = "%s weights, 4-token prompt then %d greedy tokens, batch 1" % (cfg.upper(), budget_tokens)
-    if os.path.exists(exe):
-        out = subprocess.check_output([exe, str(V), str(D), str(Ly), str(H), str(F), "1088",
-                                       str(SEED[cfg]), "4", str(budget_tokens)], env=env, text=True, timeout=600)
-        r = json.loads(out.strip().splitlines()[-1])
+    out = subprocess.check_output([exe, str(V), str(D), str(Ly), str(H), str(F), "1088",
+                                   str(SEED[cfg] if seed is None else seed), str(prompt), str(new_tokens)],
+                                  env=env, text=True, timeout=600)
+    return json.loads(out.strip().splitlines()[-1])
+
+
+def cpu_baseline(cfg, budget_tokens, prompt=32):
+    """The reference itself (oracle/_ref/ref_bench), one thread, on a bounded
+    sample of the same workload: the same model and seed, a `prompt`-token
+    prompt, then `budget_tokens` greedy steps (the generation rate excludes the
+    prompt); falls back to the oracle port if the reference build is absent."""
+    V, D, Ly, H, F, _, _ = CONFIGS[cfg]
+    sample = "%s weights, %d-token prompt then %d greedy tokens (positions %d..%d), batch 1" % (
+        cfg.upper(), prompt, budget_tokens, prompt, prompt + budget_tokens - 1)
+    r = ref_bench(cfg, prompt, budget_tokens)
+    if r is not None:
         return {"value": round(r["tok_per_s"], 3), "unit": "tokens/s", "cores": 1, "kind": "reference",
-                "sample": sample + " (masc-it/dnn.c built from its sources, NO_CBLAS scalar path)"}
+                "sample": sample + " (masc-it/dnn.c built from its sources, NO_CBLAS scalar path)",
+                "host": host_identity()}
     sys.path.insert(0, os.path.join(ROOT, "tests"))
     import oracle_lib as O
     m = O.Model(V, D, Ly, H, F, 1088, seed=SEED[cfg])
-    p = O.prompt_ids(SEED[cfg] + 100, V, 4)
+    p = O.prompt_ids(SEED[cfg] + 100, V, prompt)
     t0 = time.perf_counter()
     m.generate(p, 1)
     t_p = time.perf_counter() - t0
@@ -148,7 +185,31 @@ def cpu_baseline(cfg, budget_tokens):
     m.generate(p, budget_tokens)
     t_all = time.perf_counter() - t0
     return {"value": round((budget_tokens - 1) / (t_all - t_p), 3), "unit": "tokens/s", "cores": 1,
-            "kind": "port", "sample": sample + " (oracle/dnn_oracle.c restatement)"}
+            "kind": "port", "sample": sample + " (oracle/dnn_oracle.c restatement)", "host": host_identity()}
+
+
+def cpu_baseline_batched(cfg, B, prompt, new_tokens):
+    """The reference cannot batch generation (gpt.c:264): B independent
+    batch-1 generations, timed serially (one process) and concurrently
+    (min(B, 16) processes, one dnn_ctx each, one thread each).  Bounded
+    sample: `prompt`-token prompts, `new_tokens` greedy tokens per sequence."""
+    from concurrent.futures import ThreadPoolExecutor
+    serial = ref_bench(cfg, prompt, new_tokens)
+    if serial is None:
+        return None
+    n_par = max(1, min(B, 16, os.cpu_count() or 1))
+    t0 = time.perf_counter()
+    with ThreadPoolExecutor(max_workers=n_par) as ex:
+        runs = list(ex.map(lambda i: ref_bench(cfg, prompt, new_tokens, seed=SEED[cfg] + 1000 + i), range(n_par)))
+    wall = time.perf_counter() - t0
+    agg = sum(r["tok_per_s"] for r in runs)
+    return {"value": round(agg, 3), "unit": "tokens/s", "cores": n_par, "kind": "reference",
+            "serial_value": round(serial["tok_per_s"], 3), "serial_cores": 1,
+            "sample": "%d concurrent batch-1 generations (one process and thread each) of %s weights, "
+                      "%d-token prompt then %d greedy tokens each; value = the sum of their generation rates "
+                      "(wall %.1f s); serial_value = one such generation alone" % (
+                          n_par, cfg.upper(), prompt, new_tokens, wall),
+            "host": host_identity()}
 
 
 def decode_run(L, cfg, steps, warmup, grid=0):
@@ -180,6 +241,47 @@ def decode_run(L, cfg, steps, warmup, grid=0):
         "positions": [start_pos, start_pos + steps - 1], "P": P,
         "kernel_desc": ("dnnhip::%s (one persistent launch = %d steps)" % (KERNELS[kern], steps)) if kern in (3, 4, 5)
         else "dnnhip::%s (%d replays)" % (KERNELS.get(kern, "?"), steps),
+    }
+
+
+def run_c3(L, steps=256):
+    """the C2 model at batch 32; every row has its own
+    uniform-random 64-token prompt cut to a length drawn uniformly from
+    [16, 64] (per-row lengths), prefilled at once, then `steps` greedy steps of
+    all rows timed.  The whole workload runs twice on one session (the first
+    pass warms buffers and captures the step graph; reset in between): the
+    second pass is timed and must emit the first pass's tokens."""
+    import numpy as np
+    V, D, Ly, H, F, P, B = CONFIGS["c3"]
+    ctx, lm, dm = build_model(L, "c3", P + steps + 1)
+    r = L.dnn_rng_seed(SEED["c3"] + 100)
+    ids = np.array([[L.dnn_rng_uniform_int(C.byref(r), V) for _ in range(P)] for _ in range(B)], dtype=np.int32)
+    lens = np.array([16 + L.dnn_rng_uniform_int(C.byref(r), P - 16 + 1) for _ in range(B)], dtype=np.int32)
+    s = dnn_amd.HipSession(dm, B, P + steps + 1)
+    runs = []
+    for rep in range(2):
+        s.reset()
+        t0 = time.perf_counter()
+        nxt, _ = s.prefill(ids=ids, n_ids=lens)
+        pre_wall = time.perf_counter() - t0
+        pre_ms = s.last_ms()
+        t0 = time.perf_counter()
+        out, _ = s.decode(nxt, steps)
+        wall = time.perf_counter() - t0
+        runs.append((out, wall, s.last_ms(), pre_wall, pre_ms))
+    assert np.array_equal(runs[0][0], runs[1][0]), "c3: the timed pass emitted other tokens than the first"
+    out, wall, dev_ms, pre_wall, pre_ms = runs[1]
+    positions = [[int(lens[b]) + t for b in range(B)] for t in range(steps)]
+    nbytes = step_bytes(V, D, Ly, F, positions, B)
+    return {
+        "tok_s": B * steps / wall, "ms_per_step": wall * 1e3 / steps, "device_ms_per_step": dev_ms / steps,
+        "achieved": nbytes / (dev_ms * 1e-3) / 1e9, "nbytes": nbytes, "kernel": s.kernel(), "grid": 0, "B": B,
+        "P": P, "prompt_lens": [int(lens.min()), int(lens.max())],
+        "positions": [int(lens.min()), int(lens.max()) + steps - 1],
+        "kernel_desc": "dnnhip::%s (%d replays)" % (KERNELS.get(s.kernel(), "?"), steps),
+        "prefill": {"tokens": int(lens.sum()), "ms": round(pre_ms, 3), "wall_ms": round(pre_wall * 1e3, 3)},
+        "workload": "C3: batch 32, 64-token uniform-random prompts cut to lengths U[16,64] (%d..%d), "
+                    "ragged prefill, then %d greedy steps of every row" % (lens.min(), lens.max(), steps),
     }
 
 
@@ -324,6 +426,7 @@ def main():
     ap.add_argument("--steps", type=int, default=512)
     ap.add_argument("--warmup", type=int, default=16)
     ap.add_argument("--config", default="c2", choices=sorted(CONFIGS) + ["c4", "c5"])
+    ap.add_argument("--c3-steps", type=int, default=256, help="greedy steps of the C3 (batch 32) line")
     ap.add_argument("--grid", type=int, default=0, help="persistent-kernel workgroups (0 = one per CU)")
     ap.add_argument("--copy-probe", type=int, default=0, metavar="MIB",
                     help="after the timed decode, copy a MIB-sized device buffer 3 times (a plain copy kernel of "
@@ -340,7 +443,9 @@ def main():
     L = host_lib()
     dnn_amd.check(dnn_amd.hip().dnn_hip_init(0))
     cfg = args.config
-    if cfg == "c4":
+    if cfg == "c3":
+        r = run_c3(L, args.c3_steps if args.steps == 512 else args.steps)
+    elif cfg == "c4":
         r = run_c4(L, args)
     elif cfg == "c5":
         r = run_c5(L, args)
@@ -363,7 +468,7 @@ def main():
         "dtype": "bf16 weights / f32" if cfg == "c5" else "f32",
         "data": "synthetic: seeded N(0,0.02) weights, uniform-random prompt" + (
             ", N(0,1) patch embeddings" if cfg == "c5" else ""),
-        "config": {"workload": "%s greedy decode, batch %d" % (cfg.upper(), r["B"]),
+        "config": {"workload": r.get("workload", "%s greedy decode, batch %d" % (cfg.upper(), r["B"])),
                    "vocab": V, "d_model": D, "layers": Ly, "heads": H, "ffn": F, "prompt": r["P"],
                    "batch": r["B"], "positions": r["positions"], "grid": r["grid"]},
         "device_ms_per_step": round(r["device_ms_per_step"], 5),
@@ -374,16 +479,23 @@ def main():
     if "prefill" in r:
         line["prefill"] = r["prefill"]
     positions = range(r["positions"][0], r["positions"][1] + 1)
-    traffic = measured_traffic(cfg, positions) if cfg not in ("c4", "c5") else None
-    if traffic is not None:
-        line["roofline"]["traffic"] = traffic
+    traffic, prof = measured_traffic(cfg, positions) if cfg not in ("c4", "c5") else (None, None)
+    line["roofline"]["traffic"] = traffic
+    if prof is not None:
+        line["roofline"]["traffic_profiled_launch"] = prof
     if cfg == "c2" and not args.no_extra:
-        # the metric's second batch size, on the batched engine
-        line["c3_batch32"] = summary(decode_run(L, "c3", 256, 16))
+        # the metric's second batch size (BASELINE configs[2]), on the batched engine
+        r3 = run_c3(L, args.c3_steps)
+        line["c3_batch32"] = summary(r3)
+        line["c3_batch32"]["workload"] = r3["workload"]
+        if not args.no_cpu_baseline:
+            line["c3_batch32"]["cpu_baseline"] = cpu_baseline_batched("c3", 32, 16, 8)
     if args.copy_probe:
         copy_probe(args.copy_probe << 20)
-    if not args.no_cpu_baseline and cfg in CONFIGS and cfg not in ("c4", "c5"):
-        line["cpu_baseline"] = cpu_baseline(cfg, args.cpu_tokens)
+    if not args.no_cpu_baseline and cfg in CONFIGS and cfg not in ("c3", "c4", "c5"):
+        line["cpu_baseline"] = cpu_baseline(cfg, args.cpu_tokens, prompt=min(P, 32))
+    elif not args.no_cpu_baseline and cfg == "c3":
+        line["cpu_baseline"] = cpu_baseline_batched("c3", 32, 16, 8)
     print(json.dumps(line))
 
 
