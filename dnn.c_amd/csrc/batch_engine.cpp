@@ -479,11 +479,16 @@ int engine_decode(dnn_hip_session *s, const int *feed, int n_feed_all, const int
         e->att_spec = spec;
     }
     // the step graph, captured again when a buffer it names or a launch
-    // parameter changed
+    // parameter changed.  DNN_HIP_ENGINE_GRAPH=0 launches the step's kernels
+    // directly instead (the same kernels and arguments; every per-step value
+    // lives in device memory either way) -- for tools that trace kernel
+    // dispatches one by one.
+    const char *graph_env = getenv("DNN_HIP_ENGINE_GRAPH");
+    const bool use_graph = !(graph_env && graph_env[0] == '0');
     float *lg = logits ? s->logits : nullptr;
     const void *key[4] = {s->feed, s->ids, lg, e->X};
-    if (!e->gexec || e->geos != eos || e->gspec != e->att_spec || e->gns != e->att_ns ||
-        memcmp(key, e->gkey, sizeof key) != 0) {
+    if (use_graph && (!e->gexec || e->geos != eos || e->gspec != e->att_spec || e->gns != e->att_ns ||
+                      memcmp(key, e->gkey, sizeof key) != 0)) {
         drop_graph(e);
         HIP_TRY(hipStreamBeginCapture(s->stream, hipStreamCaptureModeThreadLocal));
         int erc = 0;
@@ -508,7 +513,18 @@ int engine_decode(dnn_hip_session *s, const int *feed, int n_feed_all, const int
     ea.pk = 1;                               // decode steps keep X in fragment order
     HIP_TRY(launch_embed(ea, s->stream));
     HIP_TRY(hipEventRecord(s->ev0, s->stream));
-    for (int t = 0; t < n_steps; t++) HIP_TRY(hipGraphLaunch(e->gexec, s->stream));
+    for (int t = 0; t < n_steps; t++) {
+        if (use_graph) {
+            HIP_TRY(hipGraphLaunch(e->gexec, s->stream));
+            continue;
+        }
+        for (int l = 0; l < m->L; l++) {
+            rc = enqueue_layer(s, l, nullptr);
+            if (rc) return rc;
+        }
+        rc = enqueue_head(s, nullptr, lg, s->ids, eos);
+        if (rc) return rc;
+    }
     HIP_TRY(hipEventRecord(s->ev1, s->stream));
     HIP_TRY(hipEventSynchronize(s->ev1));
     HIP_TRY(hipEventElapsedTime(&s->last_ms, s->ev0, s->ev1));

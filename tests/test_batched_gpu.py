@@ -63,6 +63,24 @@ def test_engine_rows_match_independent_runs(c1g, B, splits, tiles, monkeypatch):
         assert list(ids2[:, b]) == list(want[steps + 1:steps + 9]), "row %d, second call" % b
 
 
+def test_engine_without_graph_equals_graph(c1g, monkeypatch):
+    """DNN_HIP_ENGINE_GRAPH=0 launches each step's kernels directly instead of
+    replaying the captured step graph: the same tokens and logits, bit for bit."""
+    hm = hip_model(c1g)
+    rng = np.random.default_rng(77)
+    B = 16
+    lens = rng.integers(1, 9, size=B).astype(np.int32)
+    feed = rng.integers(0, 128, size=(8, B)).astype(np.int32)
+    s = A.HipSession(hm, B, 48)
+    ids_g, lg_g = s.decode(feed, 30, n_feed=lens, want_logits=True)
+    monkeypatch.setenv("DNN_HIP_ENGINE_GRAPH", "0")
+    s2 = A.HipSession(hm, B, 48)
+    ids_e, lg_e = s2.decode(feed, 30, n_feed=lens, want_logits=True)
+    assert s.kernel() == 6 and s2.kernel() == 6
+    assert np.array_equal(ids_g, ids_e)
+    assert np.array_equal(lg_g.view(np.uint32), lg_e.view(np.uint32))
+
+
 def test_engine_c2_tokens_and_logits_match_reference(golden, monkeypatch):
     """The C2 model on the engine (one row, forced): the reference's own greedy
     tokens and its logits of the first four generated steps."""
