@@ -164,9 +164,6 @@ hipError_t launch_attn(const AttnArgs &a, hipStream_t stream);
 constexpr int GEMM_KPW[] = {12, 8, 6, 4, 3, 2};
 hipError_t launch_prefill_attn(const PrefillAttnArgs &a, hipStream_t stream);
 hipError_t launch_embed(const EmbedArgs &a, hipStream_t stream);
-// y [n][out] = x [n][in] . W + b, W [in][out] (w_layout 0) or [out][in] (1); b may be null.
-hipError_t launch_linear(const float *x, int n, int in, const float *w, int w_layout, const float *b, int out, float *y,
-                         hipStream_t stream);
 hipError_t launch_rms_rows(const float *x, const float *gamma, float *y, int n, int d, int ld, float eps,
                            hipStream_t stream);
 int gemm_tile_rows(bool prefill, int M);

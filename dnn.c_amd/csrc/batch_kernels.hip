@@ -1130,31 +1130,6 @@ hipError_t launch_prefill_attn(const PrefillAttnArgs &a, hipStream_t stream) {
     return hipGetLastError();
 }
 
-namespace {
-// One thread per output (row i, column o): the k-sum in order, then the bias
-// (ops_matrix.c:1143-1151 adds the bias after the sum).  Small, one-off
-// projections (image patches); the decode path has its own GEMMs.
-__global__ __launch_bounds__(256) void linear_kernel(const float *x, int n, int in, const float *w, int w_layout,
-                                                     const float *b, int out, float *y) {
-    const int o = blockIdx.x * 256 + threadIdx.x, i = blockIdx.y;
-    if (o >= out || i >= n) return;
-    const float *xr = x + (size_t)i * in;
-    float sum = 0.f;
-    if (w_layout == 0)
-        for (int k = 0; k < in; k++) sum += xr[k] * w[(size_t)k * out + o];
-    else
-        for (int k = 0; k < in; k++) sum += xr[k] * w[(size_t)o * in + k];
-    y[(size_t)i * out + o] = sum + (b ? b[o] : 0.f);
-}
-}  // namespace
-
-hipError_t launch_linear(const float *x, int n, int in, const float *w, int w_layout, const float *b, int out, float *y,
-                         hipStream_t stream) {
-    if (n < 1 || in < 1 || out < 1 || n > 65535) return hipErrorInvalidValue;
-    hipLaunchKernelGGL(linear_kernel, dim3((out + 255) / 256, n), dim3(256), 0, stream, x, n, in, w, w_layout, b, out, y);
-    return hipGetLastError();
-}
-
 hipError_t launch_rms_rows(const float *x, const float *gamma, float *y, int n, int d, int ld, float eps,
                            hipStream_t stream) {
     hipLaunchKernelGGL(rms_rows_kernel, dim3(n), dim3(NTHR), 0, stream, x, gamma, y, d, ld, eps);

@@ -622,28 +622,7 @@ int dnn_hip_rms_norm(dnn_hip_session *s, const float *x, const float *gamma, int
 }
 
 int dnn_hip_linear(const float *x, int n, int in, const float *w, int w_layout, const float *b, int out, float *y) {
-    if (!x || !w || !y) return fail(DNN_HIP_EINVAL, "NULL argument");
-    if (n < 1 || in < 1 || out < 1 || n > 65535 || (w_layout != 0 && w_layout != 1))
-        return fail(DNN_HIP_EINVAL, "linear %d x %d -> %d (layout %d)", n, in, out, w_layout);
-    float *dx = nullptr, *dw = nullptr, *db = nullptr, *dy = nullptr;
-    int rc = dalloc(&dx, (size_t)n * in);
-    rc = rc ? rc : dalloc(&dw, (size_t)in * out);
-    rc = rc ? rc : dalloc(&dy, (size_t)n * out);
-    if (!rc && b) rc = dalloc(&db, (size_t)out);
-    hipError_t e = hipSuccess;
-    if (!rc) {
-        e = hipMemcpy(dx, x, sizeof(float) * (size_t)n * in, hipMemcpyHostToDevice);
-        if (e == hipSuccess) e = hipMemcpy(dw, w, sizeof(float) * (size_t)in * out, hipMemcpyHostToDevice);
-        if (e == hipSuccess && b) e = hipMemcpy(db, b, sizeof(float) * (size_t)out, hipMemcpyHostToDevice);
-        if (e == hipSuccess) e = launch_linear(dx, n, in, dw, w_layout, db, out, dy, nullptr);
-        if (e == hipSuccess) e = hipMemcpy(y, dy, sizeof(float) * (size_t)n * out, hipMemcpyDeviceToHost);
-    }
-    float *bufs[] = {dx, dw, db, dy};
-    for (float *p : bufs)
-        if (p) (void)hipFree(p);
-    if (rc) return rc;
-    if (e != hipSuccess) return fail(DNN_HIP_EDEVICE, "linear: %s", hipGetErrorString(e));
-    return DNN_HIP_OK;
+    return dnn_hip_op_linear(x, n, in, w, w_layout, b, out, 1, y);
 }
 
 int dnn_hip_cache_read(dnn_hip_session *s, int layer, int which, int len, float *out) {

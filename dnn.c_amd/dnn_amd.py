@@ -25,7 +25,9 @@ HIP_SYMBOLS = [
     "dnn_hip_decode", "dnn_hip_generate", "dnn_hip_session_last_ms", "dnn_hip_session_set_grid",
     "dnn_hip_session_grid", "dnn_hip_session_kernel", "dnn_hip_session_att_splits", "dnn_hip_model_create_ex", "dnn_hip_prefill",
     "dnn_hip_block_forward", "dnn_hip_head_forward", "dnn_hip_embed", "dnn_hip_cache_read", "dnn_hip_rms_norm",
-    "dnn_hip_linear",
+    "dnn_hip_linear", "dnn_hip_op_matmul_add", "dnn_hip_op_add", "dnn_hip_op_swiglu", "dnn_hip_op_rms_norm",
+    "dnn_hip_op_rope", "dnn_hip_op_embedding", "dnn_hip_op_split_heads", "dnn_hip_op_merge_heads",
+    "dnn_hip_op_linear", "dnn_hip_op_swiglu_ffn", "dnn_hip_op_cache_drop",
 ]
 
 WEIGHTS_F32 = 0

@@ -179,23 +179,6 @@ static dnn_hip_session *util_session(decoder_lm *lm) {
     return NULL;
 }
 
-/* rms_norm_forward (nn.c:169-173) over x [..., d] on the device: any model's
- * scratch session serves, the gamma comes with the call. */
-tensor *rms_norm_forward(struct mem_pool *scratch, rms_norm *norm, const tensor *x) {
-    assert(norm && x && x->contiguous && x->shape[x->ndim - 1] == norm->d);
-    decoder_lm *lm = NULL;
-    for (int i = 0; i < MAX_MODELS && !lm; i++) lm = g_models[i];
-    assert(lm && "rms_norm_forward: the device path needs a decoder_lm (for its session)");
-    const int n = tensor_numel(x) / norm->d;
-    int shape[DNN_MAX_DIMS];
-    for (int i = 0; i < x->ndim; i++) shape[i] = x->shape[i];
-    tensor *y = tensor_scratch(scratch, x->ndim, shape, 0);
-    dnn_amd_check(dnn_hip_rms_norm(util_session(lm), (const float *)x->data + x->offset, tensor_data_ptr(norm->weight), n,
-                                   norm->d, norm->eps, tensor_data_ptr(y)),
-                  "dnn_hip_rms_norm");
-    return y;
-}
-
 /* h [..., d_model] -> logits [..., V] = h . embed^T + bias (no final norm). */
 tensor *decoder_lm_lm_head_forward(struct mem_pool *scratch, decoder_lm *lm, const tensor *h) {
     assert(lm && h && h->contiguous && h->shape[h->ndim - 1] == lm->d_model);
@@ -220,56 +203,110 @@ tensor *decoder_lm_token_embeds(struct mem_pool *scratch, decoder_lm *lm, const 
     return tensor_reshape(scratch, h, 3, (int[]){B, N, lm->d_model});
 }
 
-/* B rows of N embeddings x [B][N][D] through every block (full-sequence
- * attention: an empty cache of length N per row), the final rms_norm and the
- * head, into logits [B][N][V]; a session of its own, destroyed on return. */
-static void forward_rows(decoder_lm *lm, const float *x, int B, int N, int mode, int prefix_len, float *logits) {
+/* B rows of N embeddings x [B][N][D] through layers [l0, l1) (full-sequence
+ * attention: an empty cache of length N per row) into `hidden` [B][N][D];
+ * then, with `final`, the final rms_norm -- into `hidden` (norm_only) or
+ * through the tied head into `logits` [B][N][V].  A session of its own,
+ * destroyed on return. */
+static void forward_rows(decoder_lm *lm, const float *x, int B, int N, int mode, int prefix_len, int l0, int l1,
+                         float *hidden, int final, float *logits) {
     const size_t n = (size_t)B * N * lm->d_model;
     dnn_hip_session *s = NULL;
     dnn_amd_check(dnn_hip_session_create(dnn_amd_device_model(lm), B, N, &s), "dnn_hip_session_create");
     float *a = malloc(sizeof(float) * n), *b = malloc(sizeof(float) * n);
     assert(a && b);
     memcpy(a, x, sizeof(float) * n);
-    for (int l = 0; l < lm->n_layers; l++) {
+    for (int l = l0; l < l1; l++) {
         dnn_amd_check(dnn_hip_block_forward(s, l, a, N, 0, mode, prefix_len, b), "dnn_hip_block_forward");
         float *t = a; a = b; b = t;
     }
-    dnn_amd_check(dnn_hip_head_forward(s, a, B * N, 1, logits), "dnn_hip_head_forward");
+    if (final && logits)
+        dnn_amd_check(dnn_hip_head_forward(s, a, B * N, 1, logits), "dnn_hip_head_forward");
+    else if (final)
+        dnn_amd_check(dnn_hip_op_rms_norm(a, B * N, lm->d_model, tensor_data_ptr(lm->norm->weight), lm->norm->eps, a),
+                      "dnn_hip_op_rms_norm");
+    if (hidden) memcpy(hidden, a, sizeof(float) * n);
     free(a);
     free(b);
     dnn_hip_session_destroy(s);
 }
 
+/* The rows of `in` [B][S][D] through layers [l0, l1) (+ the final norm /
+ * head), per seq_lens: batch row b runs as a sequence of its first seq_lens[b]
+ * rows (keys past it are never visible, attention.c:272,290); the rows after
+ * it, which the reference leaves uncomputed, come back zero. */
+static void forward_batch(decoder_lm *lm, const float *in, int B, int S, attention_mode mode, int prefix_len,
+                          const int *seq_lens, int l0, int l1, float *hidden, int final, float *logits) {
+    const int D = lm->d_model, V = lm->vocab_size;
+    assert((mode == ATTENTION_CAUSAL || mode == ATTENTION_PREFIX_LM) && "unknown attention mode");
+    if (!seq_lens) {
+        forward_rows(lm, in, B, S, mode, prefix_len, l0, l1, hidden, final, logits);
+        return;
+    }
+    for (int b = 0; b < B; b++) {
+        const int n = seq_lens[b];
+        assert(n >= 0 && n <= S && "seq_lens out of range");
+        float *hb = hidden ? hidden + (size_t)b * S * D : NULL;
+        float *lb = logits ? logits + (size_t)b * S * V : NULL;
+        if (n > 0) forward_rows(lm, in + (size_t)b * S * D, 1, n, mode, prefix_len, l0, l1, hb, final, lb);
+        if (hb) memset(hb + (size_t)n * D, 0, sizeof(float) * (size_t)(S - n) * D);
+        if (lb) memset(lb + (size_t)n * V, 0, sizeof(float) * (size_t)(S - n) * V);
+    }
+}
+
 /* embeds [B, S, D] -> logits [B, S, V] (gpt.c:84-144): blocks with full-sequence
- * attention (attention.c:259-380 masks), final rms_norm, tied lm_head.  With
- * seq_lens, batch row b computes its first seq_lens[b] rows as a sequence of
- * that length (keys past it are never visible, attention.c:272,290); the rows
- * after it, which the reference leaves uncomputed, are zero here. */
+ * attention (attention.c:259-380 masks), final rms_norm, tied lm_head. */
 tensor *decoder_lm_forward_embeds_ex(struct mem_pool *scratch, decoder_lm *lm, const tensor *embeds,
                                      attention_mode mode, int prefix_len, const int *seq_lens) {
     assert(lm && embeds);
     assert(embeds->ndim == 3 && "hidden_from_embeds: embeds must be 3D [B, S, D]");
     assert(embeds->shape[2] == lm->d_model && embeds->contiguous);
-    assert((mode == ATTENTION_CAUSAL || mode == ATTENTION_PREFIX_LM) && "unknown attention mode");
-    const int B = embeds->shape[0], S = embeds->shape[1], D = lm->d_model, V = lm->vocab_size;
-    const float *x = (const float *)embeds->data + embeds->offset;
+    const int B = embeds->shape[0], S = embeds->shape[1], V = lm->vocab_size;
     tensor *logits = tensor_scratch(scratch, 3, (int[]){B, S, V}, 0);
-    float *out = tensor_data_ptr(logits);
-    if (!seq_lens) {
-        forward_rows(lm, x, B, S, mode, prefix_len, out);
-        return logits;
-    }
-    for (int b = 0; b < B; b++) {
-        const int n = seq_lens[b];
-        assert(n >= 0 && n <= S && "seq_lens out of range");
-        if (n > 0) forward_rows(lm, x + (size_t)b * S * D, 1, n, mode, prefix_len, out + (size_t)b * S * V);
-        memset(out + ((size_t)b * S + n) * V, 0, sizeof(float) * (size_t)(S - n) * V);
-    }
+    forward_batch(lm, (const float *)embeds->data + embeds->offset, B, S, mode, prefix_len, seq_lens, 0,
+                  lm->n_layers, NULL, 1, tensor_data_ptr(logits));
     return logits;
 }
 
 tensor *decoder_lm_forward_embeds(struct mem_pool *scratch, decoder_lm *lm, const tensor *embeds) {
     return decoder_lm_forward_embeds_ex(scratch, lm, embeds, ATTENTION_CAUSAL, 0, NULL);
+}
+
+/* embeds [B, S, D] -> the final normalised hidden state [B, S, D] (gpt.c:84-113). */
+tensor *decoder_lm_hidden_from_embeds_ex(struct mem_pool *scratch, decoder_lm *lm, const tensor *embeds,
+                                         attention_mode mode, int prefix_len, const int *seq_lens) {
+    assert(lm && embeds);
+    assert(embeds->ndim == 3 && "hidden_from_embeds: embeds must be 3D [B, S, D]");
+    assert(embeds->shape[2] == lm->d_model && embeds->contiguous);
+    const int B = embeds->shape[0], S = embeds->shape[1], D = lm->d_model;
+    tensor *h = tensor_scratch(scratch, 3, (int[]){B, S, D}, 0);
+    forward_batch(lm, (const float *)embeds->data + embeds->offset, B, S, mode, prefix_len, seq_lens, 0, lm->n_layers,
+                  tensor_data_ptr(h), 1, NULL);
+    return h;
+}
+
+tensor *decoder_lm_hidden_from_embeds(struct mem_pool *scratch, decoder_lm *lm, const tensor *embeds) {
+    return decoder_lm_hidden_from_embeds_ex(scratch, lm, embeds, ATTENTION_CAUSAL, 0, NULL);
+}
+
+/* Full-sequence forward of one block (transformer.c:151-208), no cache. */
+tensor *transformer_block_forward_ex(struct mem_pool *scratch, transformer_block *block, const tensor *x,
+                                     attention_mode mode, int prefix_len, const int *seq_lens) {
+    assert(block && x);
+    assert(x->ndim == 3 && x->contiguous && "transformer_block_forward: x must be contiguous [B, N, d_model]");
+    assert(x->shape[2] == block->d_model);
+    int layer = -1;
+    decoder_lm *lm = model_of_block(block, &layer);
+    assert(lm && "transformer_block_forward: the block belongs to no decoder_lm (device path)");
+    const int B = x->shape[0], N = x->shape[1], D = x->shape[2];
+    tensor *y = tensor_scratch(scratch, 3, (int[]){B, N, D}, 0);
+    forward_batch(lm, (const float *)x->data + x->offset, B, N, mode, prefix_len, seq_lens, layer, layer + 1,
+                  tensor_data_ptr(y), 0, NULL);
+    return y;
+}
+
+tensor *transformer_block_forward(struct mem_pool *scratch, transformer_block *block, const tensor *x) {
+    return transformer_block_forward_ex(scratch, block, x, ATTENTION_CAUSAL, 0, NULL);
 }
 
 /* input_ids [B, N] -> logits [B, N, V] (gpt.c:148-151). */

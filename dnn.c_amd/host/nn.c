@@ -2,6 +2,8 @@
  * 40-59, 152-167, 177-191).  Creation order and bounds are the reference's, so
  * the same dnn_seed() yields the same weights. */
 #include "dnn/nn.h"
+#include "dnn/ops.h"
+#include "dnn/norm.h"
 #include "dnn_hip.h"
 #include "device.h"
 #include <assert.h>
@@ -99,21 +101,35 @@ long long linear_num_parameters(linear *l) { return module_num_parameters(&l->ba
 long long swiglu_ffn_num_parameters(swiglu_ffn *f) { return module_num_parameters(&f->base); }
 long long embedding_num_parameters(embedding *e) { return module_num_parameters(&e->base); }
 
-/* Row gather from the host table (embedding.c:79-84); the decode kernels do
- * their own gather from the HBM mirror. */
+/* embedding_forward (nn.c:193-199 -> tensor_embedding, embedding.c:63-110):
+ * the row gather runs on the device, the table resident in HBM. */
 tensor *embedding_forward(struct mem_pool *scratch, struct mem_pool *data, embedding *emb, const tensor *ids) {
     (void)data;
     assert(emb && ids && ids->ndim == 1 && "embedding: ids must be 1D");
-    const tensor *w = emb->weight;
-    assert(w->ndim == 2 && w->contiguous && "embedding: table must be 2D, contiguous");
-    const int V = w->shape[0], D = w->shape[1], N = ids->shape[0];
-    tensor *out = tensor_scratch(scratch, 2, (int[]){N, D}, 0);
-    const int *id = (const int *)ids->data + ids->offset;
-    const float *td = (const float *)w->data + w->offset;
-    for (int i = 0; i < N; i++) {
-        const int v = id[(size_t)i * ids->strides[0]];
-        assert(v >= 0 && v < V && "embedding: id out of range");
-        memcpy((float *)out->data + (size_t)i * D, td + (size_t)v * D, sizeof(float) * (size_t)D);
-    }
-    return out;
+    return tensor_embedding(scratch, emb->weight, ids);
+}
+
+/* swiglu_ffn_forward (nn.c:61-78): gate and up projections, SwiGLU, down
+ * projection, in one device call (weights resident after the first). */
+tensor *swiglu_ffn_forward(struct mem_pool *scratch, swiglu_ffn *ffn, const tensor *x) {
+    assert(ffn && x);
+    assert(x->contiguous && x->ndim >= 1 && x->shape[x->ndim - 1] == ffn->d_model &&
+           "swiglu_ffn_forward: x must be contiguous [..., d_model]");
+    const int n = tensor_numel(x) / ffn->d_model;
+    int shape[DNN_MAX_DIMS];
+    for (int i = 0; i < x->ndim; i++) shape[i] = x->shape[i];
+    tensor *y = tensor_scratch(scratch, x->ndim, shape, 0);
+    dnn_amd_check(dnn_hip_op_swiglu_ffn((const float *)x->data + x->offset, n, ffn->d_model, ffn->intermediate_size,
+                                        tensor_data_ptr(ffn->gate_proj->weight), tensor_data_ptr(ffn->gate_proj->bias),
+                                        tensor_data_ptr(ffn->up_proj->weight), tensor_data_ptr(ffn->up_proj->bias),
+                                        tensor_data_ptr(ffn->down_proj->weight), tensor_data_ptr(ffn->down_proj->bias),
+                                        tensor_data_ptr(y)),
+                  "dnn_hip_op_swiglu_ffn");
+    return y;
+}
+
+/* rms_norm_forward (nn.c:169-173 -> tensor_rms_norm) on the device. */
+tensor *rms_norm_forward(struct mem_pool *scratch, rms_norm *norm, const tensor *x) {
+    assert(norm && x && x->contiguous && x->shape[x->ndim - 1] == norm->d);
+    return tensor_rms_norm(scratch, x, norm->weight, norm->eps);
 }

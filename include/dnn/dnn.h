@@ -8,6 +8,9 @@
 #include "autograd.h"
 #include "module.h"
 #include "nn.h"
+#include "ops.h"
+#include "norm.h"
+#include "multihead.h"
 #include "attention.h"
 #include "rope.h"
 #include "tokenizer.h"

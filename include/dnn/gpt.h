@@ -41,6 +41,13 @@ tensor *decoder_lm_token_embeds(struct mem_pool *scratch, decoder_lm *lm, const 
 tensor *decoder_lm_forward_embeds_ex(struct mem_pool *scratch, decoder_lm *lm, const tensor *embeds,
                                      attention_mode mode, int prefix_len, const int *seq_lens);
 tensor *decoder_lm_forward_embeds(struct mem_pool *scratch, decoder_lm *lm, const tensor *embeds);
+/* embeds [B, S, d_model] -> the final normalised hidden state [B, S, d_model]
+ * (every block, then the final rms_norm; gpt.c:84-113), seq_lens as in
+ * decoder_lm_forward_embeds_ex (rows past a row's length come back zero).  On
+ * the device. */
+tensor *decoder_lm_hidden_from_embeds_ex(struct mem_pool *scratch, decoder_lm *lm, const tensor *embeds,
+                                         attention_mode mode, int prefix_len, const int *seq_lens);
+tensor *decoder_lm_hidden_from_embeds(struct mem_pool *scratch, decoder_lm *lm, const tensor *embeds);
 /* input_ids [B, N] int32 -> logits [B, N, V]: full causal forward (gpt.c:148-151).
  * On the device. */
 tensor *decoder_lm_forward(struct mem_pool *scratch, decoder_lm *lm, const tensor *input_ids);

@@ -58,16 +58,21 @@ conv2d     *conv2d_create(struct mem_pool *params, int in_channels, int out_chan
  * device (dnn_hip_linear). */
 tensor     *linear_forward(struct mem_pool *scratch, linear *l, const tensor *input);
 swiglu_ffn *swiglu_ffn_create(struct mem_pool *params, int d_model, int intermediate_size);
+/* swiglu_ffn_forward (nn.c:61-78): x [..., d_model] -> down(SwiGLU(gate(x), up(x)))
+ * [..., d_model], on the device (the three weights resident after the first
+ * call). */
+tensor     *swiglu_ffn_forward(struct mem_pool *scratch, swiglu_ffn *ffn, const tensor *x);
 rms_norm   *rms_norm_create(struct mem_pool *params, int d, float eps);
 embedding  *embedding_create(struct mem_pool *params, int vocab_size, int d_model);
 
 /* rms_norm_forward (nn.c:169-173): y = (x * rs) * weight per row of x [..., d].
- * On the device (needs a decoder_lm built by decoder_lm_create). */
+ * On the device. */
 tensor *rms_norm_forward(struct mem_pool *scratch, rms_norm *norm, const tensor *x);
 
 /* embedding_forward (nn.c:193-199 -> tensor_embedding, embedding.c:63-110):
- * ids [N] int32 -> rows [N, d_model] of the host table (a row copy; ids
- * outside [0, vocab) assert).  `data` is unused, as in the reference. */
+ * ids [N] int32 -> rows [N, d_model] of the table, gathered on the device
+ * (the table resident in HBM; ids outside [0, vocab) assert).  `data` is
+ * unused, as in the reference. */
 tensor *embedding_forward(struct mem_pool *scratch, struct mem_pool *data, embedding *emb, const tensor *ids);
 
 long long linear_num_parameters(linear *l);

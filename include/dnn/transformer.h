@@ -35,6 +35,18 @@ typedef struct {
 transformer_block *transformer_block_create(struct mem_pool *params_pool, int d_model, int n_heads,
                                             int d_k, int intermediate_size);
 long long transformer_block_num_parameters(transformer_block *block);
+/* Full-sequence forward of one block (transformer.c:151-208) over x [B, N,
+ * d_model] (contiguous): attention over the N rows themselves with the mode's
+ * mask (ATTENTION_CAUSAL, or ATTENTION_PREFIX_LM with prefix_len
+ * bidirectional rows), no cache.  seq_lens (nullable, [B]): row b is a
+ * sequence of its first seq_lens[b] rows; the rows after it, which the
+ * reference leaves uncomputed (attention.c:272-285), come back zero.  Runs on
+ * the device; the block must belong to a decoder_lm built by
+ * decoder_lm_create. */
+tensor *transformer_block_forward_ex(struct mem_pool *scratch, transformer_block *block, const tensor *x,
+                                     attention_mode mode, int prefix_len, const int *seq_lens);
+/* Causal full-sequence forward (transformer.c:204-208). */
+tensor *transformer_block_forward(struct mem_pool *scratch, transformer_block *block, const tensor *x);
 
 /* Cached forward of one block over x [B, N_new, d_model] (contiguous): appends
  * the new K/V to cache and attends over its rows (transformer.c:211-426).

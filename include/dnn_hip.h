@@ -176,9 +176,75 @@ int dnn_hip_cache_read(dnn_hip_session *s, int layer, int which, int len, float 
  * tensor_matmul_add) for weights the caller holds: w_layout 0 = W [in][out]
  * (the reference's linear), 1 = W [out][in] (a conv2d weight [out][C][k][k]
  * flattened, as vision_lm's patch embedding uses it, vlm.c:175-186).  b may be
- * NULL.  x, W, b, y are host memory; synchronous. */
+ * NULL.  x, W, b, y are host memory; synchronous.  W stays resident on the
+ * device (dnn_hip_op_linear with cache_w = 1). */
 int dnn_hip_linear(const float *x, int n, int in, const float *w, int w_layout, const float *b, int out,
                    float *y);
+
+/* ---- op level ------------------------------------------------------------
+ * The reference's tensor ops (ops.h, norm.h, rope.h, multihead.h) and its
+ * linear / SwiGLU FFN layers, on host tensors, computed on the device.  No
+ * model or session is needed; every call is synchronous (the result is in
+ * host memory when it returns) and serialised per device.  Operands marked
+ * cacheable (cache_* = 1: layer weights, embedding tables -- tensors that live
+ * as long as a params pool) stay resident in HBM after their first upload,
+ * keyed by host pointer, element count and a fingerprint of 4,096 sampled
+ * values; an in-place edit missing every sample needs dnn_hip_op_cache_drop.
+ * The matmul, the elementwise add, RoPE, the gather and the layout ops sum and
+ * round as the reference's NO_CBLAS loops do (k in order, bias last, no FMA
+ * contraction), so their results are the reference's bits. */
+
+#define DNN_HIP_VIEW_MAX_DIMS 8
+/* A strided view of host floats: element (i0, ..., i_{ndim-1}) is
+ * data[sum_d i_d * strides[d]] (the reference tensor's shape / strides, data
+ * already advanced by its offset).  Strides are non-negative. */
+typedef struct dnn_hip_view {
+    const float *data;
+    int ndim;
+    int shape[DNN_HIP_VIEW_MAX_DIMS];
+    int strides[DNN_HIP_VIEW_MAX_DIMS];
+} dnn_hip_view;
+
+/* tensor_matmul_add (ops.h:21, ops_matrix.c:964-1183): out = a . b + bias, or
+ * a . b^T + bias with trans_b; a [..., M, K], b [..., K, N] ([..., N, K] with
+ * trans_b), leading (batch) dimensions broadcast; bias [N] (required, as in
+ * the reference).  out: contiguous [batch..., M, N]. */
+int dnn_hip_op_matmul_add(const dnn_hip_view *a, const dnn_hip_view *b, int trans_b, const float *bias,
+                          int cache_b, float *out);
+/* tensor_add (ops.h:7, ops_elem.c:110-175): out = a + b with right-aligned
+ * broadcasting; out: contiguous, the broadcast shape. */
+int dnn_hip_op_add(const dnn_hip_view *a, const dnn_hip_view *b, float *out);
+/* tensor_swiglu (ops.h:29, ops_activation.c:283-333): out = (g / (1 + e^-g)) * u,
+ * broadcast as tensor_add. */
+int dnn_hip_op_swiglu(const dnn_hip_view *gate, const dnn_hip_view *up, float *out);
+/* tensor_rms_norm (norm.h:35, norm.c:404-495): y = (x * rs) * gamma per row of
+ * n rows x d, rs = 1/sqrtf(sum(x^2) * (1/d) + eps); gamma NULL means 1. */
+int dnn_hip_op_rms_norm(const float *x, int n, int d, const float *gamma, float eps, float *y);
+/* tensor_rope (rope.h:27, rope.c:92-144): x [outer][N][d] rotated in place,
+ * pair k of row n by cos_t/sin_t [N][d/2]. */
+int dnn_hip_op_rope(float *x, int outer, int N, int d, const float *cos_t, const float *sin_t);
+/* tensor_embedding (ops.h:63, embedding.c:63-110): out [n][D] = table[ids[i]]
+ * (table [V][D]; an id outside [0, V) is DNN_HIP_ERANGE, where the reference
+ * asserts). */
+int dnn_hip_op_embedding(const float *table, int V, int D, int cache_table, const int *ids, int n, float *out);
+/* tensor_split_qkv_heads (multihead.h:33): x [B][N][3*H*dk] -> out0/1/2
+ * [B][H][N][dk] (parts = 3); tensor_split_heads (multihead.h:20): x
+ * [B][N][H*dk] -> out0 [B][H][N][dk] (parts = 1). */
+int dnn_hip_op_split_heads(const float *x, int B, int N, int H, int dk, int parts, float *out0, float *out1,
+                           float *out2);
+/* tensor_merge_heads (multihead.h:21): x [B][H][N][dk] -> out [B][N][H*dk]. */
+int dnn_hip_op_merge_heads(const float *x, int B, int H, int N, int dk, float *out);
+/* linear_forward (nn.h:23, nn.c:27-36): y [n][out] = x [n][in] . W + b, W
+ * [in][out] (w_layout 0) or [out][in] (1); b may be NULL (zero). */
+int dnn_hip_op_linear(const float *x, int n, int in, const float *w, int w_layout, const float *b, int out,
+                      int cache_w, float *y);
+/* swiglu_ffn_forward (nn.h:45, nn.c:61-78): y [n][d_model] = down(SwiGLU(gate(x),
+ * up(x))), weights [in][out] as the reference's linears (resident after the
+ * first call), biases required. */
+int dnn_hip_op_swiglu_ffn(const float *x, int n, int d_model, int d_ffn, const float *wg, const float *bg,
+                          const float *wu, const float *bu, const float *wd, const float *bd, float *y);
+/* Drops the resident copy of one cached host operand (NULL: all of them). */
+int dnn_hip_op_cache_drop(const float *host);
 
 /* decoder_lm_generate(use_cache=1, temperature=0) for one sequence: out gets
  * prompt + generated ids (P + max_new ints), *n_out its length (stops after eos

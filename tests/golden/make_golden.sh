@@ -19,3 +19,11 @@ gcc -std=gnu11 -O2 -include stdint.h -I"$REF/include" -I"$REF/src" -w \
     tests/golden/gen_ckpt.c -o oracle/_ref/gen_ckpt \
     -Loracle/_ref -ldnnref -Wl,-rpath,"$PWD/oracle/_ref" -lm
 OMP_NUM_THREADS=1 ./oracle/_ref/gen_ckpt
+# op- and layer-level fixtures: tests/c/ops_main.c is a caller of the public API
+# only, built here against the reference and in tests/test_ops_gpu.py against
+# include/dnn + libdnn_amd.so
+gcc -std=gnu11 -O2 -include stdint.h -I"$REF/include" -I"$REF/src" -w \
+    tests/c/ops_main.c -o oracle/_ref/ops_main \
+    -Loracle/_ref -ldnnref -Wl,-rpath,"$PWD/oracle/_ref" -lm
+mkdir -p tests/golden/data/ops
+OMP_NUM_THREADS=1 ./oracle/_ref/ops_main tests/golden/data/ops
