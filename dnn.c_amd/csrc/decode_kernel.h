@@ -95,8 +95,9 @@ struct DecodeArgs {
     float *logits;          // [n_steps][B][V] or null
     int n_steps, eos;
     unsigned step0;         // tag of this launch's first step (>= 1, increasing)
-    int *err;               // bit 0: a dependency wait hit its spin cap
+    int *err;               // bit 0: a dependency wait hit its spin cap; bit 1: a row had no room
     int *steps_done;
+    int seq_limit;          // length + n_steps <= this for every row (max_seq, RoPE rows)
 };
 
 // Dynamic LDS of the decode kernel (bytes): per-row token / position / done

@@ -157,6 +157,19 @@ __device__ __forceinline__ void decode_v3_body(const DecodeArgs &a, const int G,
         s_tok[b] = 0;
     }
     __syncthreads();
+    // every row must have room for the launch's steps (the host checks this
+    // where it knows the lengths; callers that keep them on the device rely on
+    // this): otherwise every workgroup leaves before touching anything, and
+    // the launch reports error bit 1
+    bool room = true;
+    for (int b = 0; b < B; b++) room &= s_pos[b] >= 0 && s_pos[b] + a.n_steps <= a.seq_limit;
+    if (!room) {
+        if (g0 == 0 && tid == 0) {
+            atomicOr(a.err, 2);
+            *a.steps_done = 0;
+        }
+        return;
+    }
 
     int t = 0;
     for (; t < a.n_steps; t++) {

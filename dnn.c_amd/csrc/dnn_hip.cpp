@@ -167,7 +167,7 @@ int dnn_hip_init(int device) {
     HIP_TRY(hipGetDeviceCount(&n));
     if (device < 0 || device >= n) return fail(DNN_HIP_EINVAL, "device %d of %d", device, n);
     HIP_TRY(hipSetDevice(device));
-    return DNN_HIP_OK;
+    return dnnhip::static_scratch_setup(device);
 }
 
 int dnn_hip_model_create(int V, int D, int L, int H, int dk, int F, const float *const *params,
@@ -397,6 +397,23 @@ int dnn_hip_session_last_ms(dnn_hip_session *s, float *ms) {
 }
 
 extern "C++" {
+// Workgroups per (row, head) of decode_v3's attention in a launch whose rows
+// reach at most pmax positions: enough that each wavefront walks at most 4
+// 32-key chunks (measured on the C2 shape: a split costs the out_proj
+// workgroups more staging than it saves below that), no more than the
+// workgroups idle during the QKV phase (so every split starts its key loads
+// with the layer), and at most ns_cap; req > 0 fixes it instead.
+int dnnhip::att_splits_for(const dnn_hip_model *m, int B, int ns_cap, int req, int grid, int pmax) {
+    const int heads = B * m->H;
+    if (ns_cap <= 1) return 1;
+    if (req > 0) return std::min(req, ns_cap);
+    const int nch = (pmax + CH - 1) / CH;
+    const int idle = grid - std::min(grid, (3 * m->D / 2 + WPB - 1) / WPB);
+    int ns = std::min(ns_cap, (nch + 4 * WPB - 1) / (4 * WPB));
+    while (ns > 1 && heads * ns > idle) ns--;
+    return std::max(ns, 1);
+}
+
 int dnnhip::stage_begin(dnn_hip_session *s, size_t bytes) {
     s->stage_used = 0;
     if (bytes <= s->stage_cap) return DNN_HIP_OK;
@@ -474,17 +491,9 @@ namespace {
 // with the layer), and at most ATT_SPLIT_MAX; DNN_HIP_ATT_SPLITS fixes it
 // instead.
 int att_splits(const dnn_hip_session *s, int grid, int n_steps) {
-    const dnn_hip_model *m = s->m;
-    const int heads = s->B * m->H;
-    if (s->ex.ns <= 1) return 1;
-    if (s->att_splits_req > 0) return std::min(s->att_splits_req, s->ex.ns);
     int pmax = 0;
     for (int b = 0; b < s->B; b++) pmax = std::max(pmax, s->h_pos[b] + n_steps);
-    const int nch = (pmax + CH - 1) / CH;
-    const int idle = grid - std::min(grid, (3 * m->D / 2 + WPB - 1) / WPB);
-    int ns = std::min(s->ex.ns, (nch + 4 * WPB - 1) / (4 * WPB));
-    while (ns > 1 && heads * ns > idle) ns--;
-    return std::max(ns, 1);
+    return dnnhip::att_splits_for(s->m, s->B, s->ex.ns, s->att_splits_req, grid, pmax);
 }
 
 // Validate and enqueue one launch of a persistent decode kernel on the
@@ -550,6 +559,7 @@ int decode_launch(dnn_hip_session *s, const int *feed, int n_feed_all, const int
     a.pos = s->pos; a.feed = s->feed; a.n_feed = s->n_feed;
     a.ids = s->ids; a.logits = want_logits ? s->logits : nullptr;
     a.n_steps = n_steps; a.eos = eos; a.step0 = s->next_tag; a.err = s->err; a.steps_done = s->steps_done;
+    a.seq_limit = m->rope ? std::min(s->max_seq, m->rope_rows) : s->max_seq;
     s->next_tag += (unsigned)n_steps;
     void *kargs[] = {&a};
     HIP_TRY(hipEventRecord(s->ev0, s->stream));

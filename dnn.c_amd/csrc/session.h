@@ -137,6 +137,12 @@ int stage_copy2d(dnn_hip_session *s, void *dst, size_t dpitch, const void *src, 
                  size_t rows);
 inline size_t stage_size(size_t bytes) { return (bytes + 255) / 256 * 256; }
 
+// workgroups per (row, head) of the persistent kernel's attention (dnn_hip.cpp)
+int att_splits_for(const dnn_hip_model *m, int B, int ns_cap, int req, int grid, int pmax);
+// the static exchange arena of dnn_hip_decode_static on the current device
+// (decode_static.hip): its device address is looked up once per device
+int static_scratch_setup(int device);
+
 // argument checks of dnn_hip_decode: nf[b] = feed rows of row b
 int check_decode(dnn_hip_session *s, const int *feed, int n_feed_all, const int *n_feed, int n_steps,
                  std::vector<int> &nf, int *nf_max);

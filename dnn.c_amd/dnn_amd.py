@@ -28,6 +28,7 @@ HIP_SYMBOLS = [
     "dnn_hip_linear", "dnn_hip_op_matmul_add", "dnn_hip_op_add", "dnn_hip_op_swiglu", "dnn_hip_op_rms_norm",
     "dnn_hip_op_rope", "dnn_hip_op_embedding", "dnn_hip_op_split_heads", "dnn_hip_op_merge_heads",
     "dnn_hip_op_linear", "dnn_hip_op_swiglu_ffn", "dnn_hip_op_cache_drop",
+    "dnn_hip_kv_floats", "dnn_hip_decode_static", "dnn_hip_decode_static_status",
 ]
 
 WEIGHTS_F32 = 0

@@ -273,6 +273,45 @@ int dnn_hip_session_kernel(dnn_hip_session *s, int *which);
  * fixed by the environment variable DNN_HIP_ATT_SPLITS at session creation). */
 int dnn_hip_session_att_splits(dnn_hip_session *s, int *splits);
 
+/* ---- decode without allocation (no counterpart in the reference) ----------
+ * For callers that cannot allocate device memory -- code under HIP graph
+ * capture, tight serving loops, harnesses that forbid hipMalloc: the
+ * persistent decode kernel of dnn_hip_decode on buffers the caller owns, its
+ * scratch (exchange arena and status words) in a fixed device array of the
+ * library (DNN_HIP_STATIC_EXCHANGE_PAIRS pairs of 8 bytes, held on each GPU
+ * the library runs on until the process ends).  Nothing is allocated and the
+ * host is not synchronised: the work is enqueued on `stream` (a hipStream_t;
+ * NULL = the null stream).  Every call on one GPU shares that array, so calls
+ * that overlap on one GPU race; run them on one stream (or order them). */
+#define DNN_HIP_STATIC_EXCHANGE_PAIRS ((size_t)1 << 20)
+
+/* Floats in each of the K and V cache buffers a dnn_hip_decode_static call
+ * of this model, batch and max_seq reads and writes (0 on bad arguments). */
+size_t dnn_hip_kv_floats(const dnn_hip_model *m, int batch, int max_seq);
+
+/* dnn_hip_decode's greedy loop for 1..8 rows of an fp32-weight model, every
+ * buffer on the device and owned by the caller:
+ *   kc, vc     K and V caches of dnn_hip_kv_floats(m, batch, max_seq) floats
+ *              each (no initialisation needed)
+ *   pos        [batch] cached length of each row, advanced by the steps run
+ *   feed       [n_feed_rows][batch], n_feed [batch]: as dnn_hip_decode
+ *   ids        [n_steps][batch] greedy ids; logits [n_steps][batch][V] or NULL
+ *   max_len    a bound the caller guarantees: every row's length + n_steps <=
+ *              max_len <= max_seq (and <= the RoPE rows); it sizes the
+ *              attention split, and a row past it stops the launch with error
+ *              bit 2 before anything is written
+ * Sizes beyond the static arena (model and batch needing more than
+ * DNN_HIP_STATIC_EXCHANGE_PAIRS pairs) are DNN_HIP_EINVAL.  The device status
+ * of the last call is read with dnn_hip_decode_static_status. */
+int dnn_hip_decode_static(dnn_hip_model *m, int batch, int max_seq, float *kc, float *vc, int *pos,
+                          const int *feed, const int *n_feed, int n_steps, int eos, int max_len, int *ids,
+                          float *logits, void *stream);
+/* Waits for `stream`, then reports the last dnn_hip_decode_static call on the
+ * current device: *steps_done (steps run; fewer when every row hit eos) and
+ * *err_bits (1: a dependency wait timed out, 2: a row had no room); returns
+ * DNN_HIP_EDEVICE when an error bit is set. */
+int dnn_hip_decode_static_status(void *stream, int *steps_done, int *err_bits);
+
 #ifdef __cplusplus
 }
 #endif
