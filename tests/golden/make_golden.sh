@@ -27,3 +27,13 @@ gcc -std=gnu11 -O2 -include stdint.h -I"$REF/include" -I"$REF/src" -w \
     -Loracle/_ref -ldnnref -Wl,-rpath,"$PWD/oracle/_ref" -lm
 mkdir -p tests/golden/data/ops
 OMP_NUM_THREADS=1 ./oracle/_ref/ops_main tests/golden/data/ops
+# sampled generation (temperature > 0): the reference's ids and each draw's
+# distance to its CDF interval's edges
+gcc -std=gnu11 -O2 -include stdint.h -I"$REF/include" -I"$REF/src" -w \
+    tests/golden/gen_sample.c -o oracle/_ref/gen_sample \
+    -Loracle/_ref -ldnnref -Wl,-rpath,"$PWD/oracle/_ref" -lm
+OMP_NUM_THREADS=1 ./oracle/_ref/gen_sample
+# the byte tokenizer: tests/c/tok_main.c against the reference
+gcc -std=gnu11 -O2 -include stdint.h -I"$REF/include" -I"$REF/src" -w \
+    tests/c/tok_main.c -o oracle/_ref/tok_main -Loracle/_ref -ldnnref -Wl,-rpath,"$PWD/oracle/_ref" -lm
+./oracle/_ref/tok_main > tests/golden/data/tokenizer.json

@@ -63,3 +63,20 @@ def test_dnnm_checkpoint_round_trip(ckpt_main, tmp_path):
     assert r["reloaded"] == g["ckpt_params"]
     with open(ref, "rb") as a, open(out, "rb") as b:
         assert a.read() == b.read()
+
+
+def test_tokenizer_matches_reference(built, tmp_path):
+    """tests/c/tok_main.c (the reference's tokenizer API only) built against
+    include/dnn prints what the same file printed built against the reference:
+    byte ids with BOS/EOS, the chat template's special strings (and a
+    truncated one left as bytes), decode dropping BOS/EOS/PAD and mapping
+    other ids to '?', the tensor round trip, empty input."""
+    exe = str(tmp_path / "tok_main")
+    libdir = os.path.join(ROOT, "dnn.c_amd", "lib")
+    subprocess.check_call(["gcc", "-std=gnu11", "-O2", "-Wall", "-I" + os.path.join(ROOT, "include", "dnn"),
+                           os.path.join(ROOT, "tests", "c", "tok_main.c"), "-o", exe,
+                           "-L" + libdir, "-ldnn_amd", "-Wl,-rpath," + libdir, "-lm"])
+    got = subprocess.check_output([exe], text=True, timeout=60)
+    with open(os.path.join(ROOT, "tests", "golden", "data", "tokenizer.json")) as f:
+        want = f.read()
+    assert json.loads(got) == json.loads(want)
