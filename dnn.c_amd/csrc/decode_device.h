@@ -91,6 +91,11 @@ __device__ __forceinline__ float bcast(float v, int lane) {
     return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), lane));
 }
 
+// Workgroup barrier for hand-offs through LDS only: waits for this wavefront's
+// LDS operations, not for its vector-memory ones (__syncthreads' fence also
+// drains vmcnt), so weight loads issued for a later phase stay in flight.
+__device__ __forceinline__ void lds_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
+
 // Bounded wait bookkeeping: once any wait gives up, err[0] is set and every
 // later wait returns at once, so all waves run to the end of the launch.
 struct Waiter {
@@ -210,6 +215,50 @@ __device__ __forceinline__ void load_rows(f4 (&w)[R][DC], rsrc_t rw, size_t off,
     for (int r = 0; r < R; r++)
 #pragma unroll
         for (int k = 0; k < DC; k++) w[r][k] = ld4<CP_NT>(rw, (off + (size_t)r * ld + k * 256 + 4 * lane) * 4);
+}
+
+// Per-lane partial sums of dot_lds, before the wavefront reduction:
+// s[r * NB + b] = this lane's share of w[r] . y_b.
+template <int R, int NB, int DC, bool NORM>
+__device__ __forceinline__ void part_lds(const f4 (&w)[R][DC], const float *xs, int ld, const float (&rs)[NB],
+                                         const f4 (&g)[DC], int lane, float *s) {
+#pragma unroll
+    for (int b = 0; b < NB; b++) {
+#pragma unroll
+        for (int r = 0; r < R; r++) s[r * NB + b] = 0.f;
+#pragma unroll
+        for (int k = 0; k < DC; k++) {
+            f4 y = *reinterpret_cast<const f4 *>(xs + b * ld + k * 256 + 4 * lane);
+            if (NORM) {
+                y.x = (y.x * rs[b]) * g[k].x; y.y = (y.y * rs[b]) * g[k].y;
+                y.z = (y.z * rs[b]) * g[k].z; y.w = (y.w * rs[b]) * g[k].w;
+            }
+#pragma unroll
+            for (int r = 0; r < R; r++)
+                s[r * NB + b] += w[r][k].x * y.x + w[r][k].y * y.y + w[r][k].z * y.z + w[r][k].w * y.w;
+        }
+    }
+}
+
+// N independent wave sums with their DPP steps interleaved (no hazard wait
+// states between dependent steps); each value gets the same additions in the
+// same order as wave_sum.
+template <int N>
+__device__ __forceinline__ void wave_sum_n(float *v) {
+#pragma unroll
+    for (int i = 0; i < N; i++) v[i] += dpp<0xb1, 0xf>(v[i], 0.f);
+#pragma unroll
+    for (int i = 0; i < N; i++) v[i] += dpp<0x4e, 0xf>(v[i], 0.f);
+#pragma unroll
+    for (int i = 0; i < N; i++) v[i] += dpp<0x141, 0xf>(v[i], 0.f);
+#pragma unroll
+    for (int i = 0; i < N; i++) v[i] += dpp<0x140, 0xf>(v[i], 0.f);
+#pragma unroll
+    for (int i = 0; i < N; i++) v[i] += dpp<0x142, 0xa>(v[i], 0.f);
+#pragma unroll
+    for (int i = 0; i < N; i++) v[i] += dpp<0x143, 0xc>(v[i], 0.f);
+#pragma unroll
+    for (int i = 0; i < N; i++) v[i] = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v[i]), 63));
 }
 
 // acc[r][b] = sum_k w[r][k] . y_b[k], y_b = LDS row b, optionally normalised

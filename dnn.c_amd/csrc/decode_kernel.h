@@ -15,6 +15,12 @@ constexpr int MAXB = 8;           // batch rows per decode launch
 constexpr int MAX_ROWS = 64;      // rows per session (more than MAXB: the batched engine)
 constexpr int LDALIGN = 256;      // weight rows / activation rows padded to this many floats
 constexpr int FCMAX = 8;          // down-projection input chunks of 256: d_ffn <= 2048
+constexpr int PU = 4;             // GEMV rounds of 2-row units a wavefront holds ahead of a phase
+constexpr int PE = 2;             // down-projection rounds (rows of d_ffn) held ahead
+constexpr int CPW = 2;            // attention chunks a wavefront loads per pass
+
+// Workgroup roles of the persistent decode kernel (see plan_roles)
+enum { R_AC = 0, R_ATT = 1, R_D = 2, R_E = 3 };
 
 // One transformer block inside the weight arena, as float offsets from its
 // base.  Weight matrices are out-major: row n holds the K inputs of output n,
@@ -98,14 +104,54 @@ struct DecodeArgs {
     int *err;               // bit 0: a dependency wait hit its spin cap; bit 1: a row had no room
     int *steps_done;
     int seq_limit;          // length + n_steps <= this for every row (max_seq, RoPE rows)
+    int n_ac, n_d, n_e;     // workgroups of the A+C, D and E roles (plan_roles); the rest attention
 };
 
+// Split of a grid of G workgroups into the kernel's roles: n_ac run the QKV
+// and out_proj GEMVs, n_d gate/up, n_e down, and the rest (at least
+// min(att_records, G / 5), at least 1) attention.  Among the splits that fit,
+// the one whose largest per-wavefront weight share of a phase (rounds x unit
+// length) is smallest, then the fewest rounds in total, then the most
+// workgroups.  Returns false when G cannot hold one workgroup per role.
+struct Roles {
+    int n_ac, n_d, n_e;
+};
+inline bool plan_roles(int G, int D, int F, int ldD, int ldF, int att_records, Roles &out) {
+    const int n_att = att_records < G / 5 ? (att_records > 1 ? att_records : 1) : (G / 5 > 1 ? G / 5 : 1);
+    const int R = G - n_att;
+    if (R < 3) return false;
+    const int nuA = 3 * D / 2, nuC = D / 2, nuD = F, nuE = D;
+    auto cdiv = [](long x, long y) { return (int)((x + y - 1) / y); };
+    long best_cost = -1;
+    int best_rounds = 0, best_used = 0;
+    for (int ra = 1; ra <= 16; ra++)
+        for (int rd = 1; rd <= 32; rd++)
+            for (int re = 1; re <= 16; re++) {
+                const int nac = cdiv(nuA, (long)WPB * ra), nd = cdiv(nuD, (long)WPB * rd), ne = cdiv(nuE, (long)WPB * re);
+                const int used = nac + nd + ne;
+                if (used > R) continue;
+                const int rc = cdiv(nuC, (long)WPB * nac);
+                long cost = (long)ra * 2 * ldD;
+                if ((long)rc * 2 * ldD > cost) cost = (long)rc * 2 * ldD;
+                if ((long)rd * 2 * ldD > cost) cost = (long)rd * 2 * ldD;
+                if ((long)re * ldF > cost) cost = (long)re * ldF;
+                const int rounds = ra + rc + rd + re;
+                const bool better = best_cost < 0 || cost < best_cost ||
+                                    (cost == best_cost && (rounds < best_rounds || (rounds == best_rounds && used > best_used)));
+                if (better) {
+                    best_cost = cost; best_rounds = rounds; best_used = used;
+                    out = Roles{nac, nd, ne};
+                }
+            }
+    return best_cost >= 0;
+}
+
 // Dynamic LDS of the decode kernel (bytes): per-row token / position / done
-// flags, per-wavefront argmax and attention partials, the double-buffered
-// output block of a GEMV round (OUT [2][WPB][2*MAXB]), each attention
-// wavefront's query and chunk weights (QE [WPB][DK + CH]), then the staged rows
+// flags, per-wavefront argmax and attention partials, the output blocks of PU
+// GEMV rounds (OUT [PU][WPB][2*MAXB]), each attention
+// wavefront's query and chunk weights (QE [WPB][DK + CPW*CH]), then the staged rows
 // XS (layer input), AS (attention), X1S and ACTS, nb rows each.
-constexpr int LDS_HEAD_WORDS = 3 * MAXB + 2 * WPB * MAXB + WPB * (DK + 2) + 2 * WPB * 2 * MAXB + WPB * (DK + CH);
+constexpr int LDS_HEAD_WORDS = 3 * MAXB + 2 * WPB * MAXB + WPB * (DK + 2) + PU * WPB * 2 * MAXB + WPB * (DK + CPW * CH);
 inline size_t lds_bytes(int nb, int ldD, int ldF) {
     return (size_t)4 * ((LDS_HEAD_WORDS + 3) / 4 * 4) + (size_t)4 * nb * (3 * (size_t)ldD + ldF);
 }

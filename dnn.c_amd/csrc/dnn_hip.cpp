@@ -400,17 +400,16 @@ extern "C++" {
 // Workgroups per (row, head) of decode_v3's attention in a launch whose rows
 // reach at most pmax positions: enough that each wavefront walks at most 4
 // 32-key chunks (measured on the C2 shape: a split costs the out_proj
-// workgroups more staging than it saves below that), no more than the
-// workgroups idle during the QKV phase (so every split starts its key loads
-// with the layer), and at most ns_cap; req > 0 fixes it instead.
+// workgroups more staging than it saves below that), records of at most a
+// fifth of the grid (the attention role's share), and at most ns_cap; req > 0
+// fixes it instead.
 int dnnhip::att_splits_for(const dnn_hip_model *m, int B, int ns_cap, int req, int grid, int pmax) {
     const int heads = B * m->H;
     if (ns_cap <= 1) return 1;
     if (req > 0) return std::min(req, ns_cap);
     const int nch = (pmax + CH - 1) / CH;
-    const int idle = grid - std::min(grid, (3 * m->D / 2 + WPB - 1) / WPB);
     int ns = std::min(ns_cap, (nch + 4 * WPB - 1) / (4 * WPB));
-    while (ns > 1 && heads * ns > idle) ns--;
+    while (ns > 1 && heads * ns > grid / 5) ns--;     // the attention role's share of the grid
     return std::max(ns, 1);
 }
 
@@ -483,13 +482,9 @@ int dnnhip::check_decode(dnn_hip_session *s, const int *feed, int n_feed_all, co
 
 namespace {
 
-// Workgroups per (row, head) of decode_v3's attention in a launch of n_steps:
-// enough that each wavefront walks at most 4 32-key chunks of the longest
-// history the launch reaches (measured on the C2 shape: a split costs the
-// out_proj workgroups more staging than it saves below that), no more than the
-// workgroups idle during the QKV phase (so every split starts its key loads
-// with the layer), and at most ATT_SPLIT_MAX; DNN_HIP_ATT_SPLITS fixes it
-// instead.
+// Workgroups per (row, head) of decode_v3's attention in a launch of n_steps,
+// from the longest history the launch reaches (att_splits_for);
+// DNN_HIP_ATT_SPLITS fixes it instead.
 int att_splits(const dnn_hip_session *s, int grid, int n_steps) {
     int pmax = 0;
     for (int b = 0; b < s->B; b++) pmax = std::max(pmax, s->h_pos[b] + n_steps);
@@ -560,6 +555,10 @@ int decode_launch(dnn_hip_session *s, const int *feed, int n_feed_all, const int
     a.ids = s->ids; a.logits = want_logits ? s->logits : nullptr;
     a.n_steps = n_steps; a.eos = eos; a.step0 = s->next_tag; a.err = s->err; a.steps_done = s->steps_done;
     a.seq_limit = m->rope ? std::min(s->max_seq, m->rope_rows) : s->max_seq;
+    Roles roles{};
+    if (!plan_roles(grid, m->D, m->F, m->ldD, m->ldF, B * m->H * a.ex.ns, roles))
+        return fail(DNN_HIP_EINVAL, "a grid of %d workgroups is too small for the decode kernel's roles", grid);
+    a.n_ac = roles.n_ac; a.n_d = roles.n_d; a.n_e = roles.n_e;
     s->next_tag += (unsigned)n_steps;
     void *kargs[] = {&a};
     HIP_TRY(hipEventRecord(s->ev0, s->stream));
