@@ -47,10 +47,11 @@ struct LayerOff {
 //   X1 [ldD]  residual stream after attention    X2 [ldD]  after the FFN
 //   Q, KN, VN [D]  this step's query and new key/value rows (after RoPE)
 //   ATT [D]   merged attention heads            ACT [ldF] SwiGLU output
-// then the lm_head argmax partials AMAX [2][B][grid][2] (value, index), double
-// buffered by step parity: a workgroup overwrites its step-t slot at step t+2
-// only after reading every workgroup's step-(t+1) partial, each written after
-// its writer finished reading the step-t partials.  When a head's keys are
+// then the lm_head argmax partials AMAX [2][B][grid][2] (value, index) and the
+// reduced tokens TOK [2][8 copies][16] (one copy per XCD, a cache line each),
+// both double buffered by step parity: a step-(t+2) slot is written only after
+// the lm_head of step t+2 ran, which needs every workgroup that reads a step-t
+// slot to have finished step t+1.  When a head's keys are
 // split over ns > 1 workgroups, the attention partials follow, per layer:
 //   AO [B*H*ns][DK]  sum_j e^(s_j - m) v_j of record r = (b*H + h)*ns + split
 //   AML [B*H*ns][2]  (m, sum_j e^(s_j - m)) of the same record
@@ -72,9 +73,12 @@ struct Exch {
     __host__ __device__ size_t amax(int L, int par, int b, int g) const {
         return per_layer() * L + (((size_t)par * B + b) * grid + g) * 2;
     }
+    __host__ __device__ size_t tok(int L, int par, int copy, int b) const {
+        return per_layer() * L + (size_t)2 * B * grid * 2 + ((size_t)par * 8 + copy) * 16 + b;
+    }
     __host__ __device__ size_t nrec() const { return ns > 1 ? (size_t)B * H * ns : 0; }
     __host__ __device__ size_t ao(int L, int l) const {
-        return per_layer() * L + (size_t)2 * B * grid * 2 + (size_t)l * nrec() * (DK + 2);
+        return per_layer() * L + (size_t)2 * B * grid * 2 + 2 * 8 * 16 + (size_t)l * nrec() * (DK + 2);
     }
     __host__ __device__ size_t aml(int L, int l) const { return ao(L, l) + nrec() * DK; }
     __host__ __device__ size_t total(int L) const { return ao(L, L); }

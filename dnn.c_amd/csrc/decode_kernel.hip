@@ -165,16 +165,16 @@ __device__ __forceinline__ void decode_v3_body(const DecodeArgs &a, const int G,
     const float scale = 1.0f / sqrtf((float)DK);
 
     // roles: [0, n_ac) A+C, then n_d D, n_e E, the rest attention; the lm_head
-    // runs on the A+C workgroups, then the E ones (index fi of nF)
+    // runs on the D workgroups, then the E ones (index fi of nF)
     const int nAC = a.n_ac, nDD = a.n_d, nEE = a.n_e;
     const int nAT = G - nAC - nDD - nEE;
-    const int nF = nAC + nEE;
+    const int nF = nDD + nEE;
     int role, r0;
     if (g0 < nAC) { role = R_AC; r0 = g0; }
     else if (g0 < nAC + nDD) { role = R_D; r0 = g0 - nAC; }
     else if (g0 < nAC + nDD + nEE) { role = R_E; r0 = g0 - nAC - nDD; }
     else { role = R_ATT; r0 = g0 - nAC - nDD - nEE; }
-    const int fi = role == R_AC ? r0 : nAC + r0;                // lm_head index (A+C and E roles)
+    const int fi = role == R_D ? r0 : nDD + r0;                 // lm_head index (D and E roles)
 
     for (int i = tid; i < NB * (3 * ldD + ldF); i += BLOCK) xs[i] = 0.f;
     for (int b = tid; b < MAXB; b += BLOCK) {
@@ -199,6 +199,10 @@ __device__ __forceinline__ void decode_v3_body(const DecodeArgs &a, const int G,
 
     int t = 0;
     bool pre = false;                                            // A+C role: layer 0's units held
+
+    // attention workgroups without a record (other than the reducer) have
+    // nothing to do: nothing waits for them
+    if (role == R_ATT && r0 >= B * H * ns && r0 != nAT - 1) return;
 
     auto nrounds = [&](int nu, int n) { return (nu + n * WPB - 1) / (n * WPB); };
     auto unit = [&](int k, int n) { return (k * n + r0) * WPB + wid; };
@@ -278,10 +282,14 @@ __device__ __forceinline__ void decode_v3_body(const DecodeArgs &a, const int G,
     };
 
 
-    // ---- G: every workgroup reduces the lm_head partials -> next token (the
-    // same in all); wavefront w reduces rows w, w + 8, ...
+    // ---- G: the last attention workgroup reduces the lm_head partials (its
+    // wavefront w takes rows w, w + 8, ...; first index of the maximum,
+    // gpt.c:220-230) and writes each row's token in 8 copies, one per XCD;
+    // every workgroup then polls its XCD's copy (one cache line per XCD
+    // instead of every partial polled by every workgroup).
+    const bool reducer = role == R_ATT && r0 == nAT - 1;
     auto reduce_g = [&](unsigned tag) {
-        for (int b = wid; b < B; b += WPB) {
+        for (int b = wid; reducer && b < B; b += WPB) {
             float v = -INFINITY;
             int i = 0x7fffffff;
             // every partial in one polling pass (4 per lane)
@@ -313,8 +321,13 @@ __device__ __forceinline__ void decode_v3_body(const DecodeArgs &a, const int G,
                 const int ii = __shfl_xor(i, o, WAVE);
                 if (vv > v || (vv == v && ii < i)) { v = vv; i = ii; }
             }
-            if (lane == 0) {
-                if (i < 0 || i >= V) i = 0;     // all-NaN row: argmax keeps index 0
+            if (i < 0 || i >= V) i = 0;         // all-NaN row: argmax keeps index 0
+            if (lane < 8) put(xa, a.ex.tok(a.L, t & 1, lane, b), __builtin_bit_cast(float, i), tag);
+        }
+        if (wid == 0) {
+            const int b = lane < B ? lane : 0;
+            const int i = __builtin_bit_cast(int, poll1(xa, (long)a.ex.tok(a.L, t & 1, g0 & 7, b), tag, wt));
+            if (lane < B) {
                 s_tok[b] = i;
                 s_pos[b] += 1;
                 if (a.eos >= 0 && t >= a.n_feed[b] - 1 && i == a.eos) s_done[b] = 1;
@@ -332,7 +345,7 @@ __device__ __forceinline__ void decode_v3_body(const DecodeArgs &a, const int G,
     };
 
     // ---- F: final rms_norm -> tied lm_head + bias -> this workgroup's argmax
-    // partial (A+C and E roles; their first PH rounds were loaded a phase or
+    // partial (D and E roles; their first PH rounds were loaded a phase or
     // more ahead)
     auto lm_head = [&](unsigned tag) {
         TRACE_EV(a.L, 0);
@@ -499,25 +512,16 @@ __device__ __forceinline__ void decode_v3_body(const DecodeArgs &a, const int G,
                     write_block<2, NB>(out, xa, a.ex.x1(l, 0), xstride, u0, nuC, B, tag, lane);
                 }, l, 11);
                 TRACE_EV(l, 5);
-                // the next layer's first A rounds, loaded while D and E run
-                // (after the last layer: the lm_head's)
-                if (l + 1 < a.L) {
-                    const LayerOff wn = load_layer(a.layers + l + 1);
-                    prefetch(nuA, nAC, [&](int j, int u) { load_a(j, wn, u, 0); });
+                // the next layer's first A rounds (after the last layer: layer 0
+                // of the next step, at the next position), loaded while D, E and
+                // the lm_head run
+                {
+                    const bool last = l + 1 == a.L;
+                    const LayerOff wn = load_layer(a.layers + (last ? 0 : l + 1));
+                    prefetch(nuA, nAC, [&](int j, int u) { load_a(j, wn, u, last ? 1 : 0); });
                     load_gamma<DC>(gp, rw, wn.g_attn, lane);
                     pre = true;
-                } else {
-                    prefetch_f();
                 }
-            }
-            lm_head(tag);
-            // layer 0 of the next step (at the next position), loaded while the
-            // lm_head partials are gathered
-            {
-                const LayerOff w0 = load_layer(a.layers);
-                prefetch(3 * D / 2, nAC, [&](int j, int u) { load_a(j, w0, u, 1); });
-                load_gamma<DC>(gp, rw, w0.g_attn, lane);
-                pre = true;
             }
             if (reduce_g(tag)) { t++; break; }
         }
@@ -701,23 +705,24 @@ __device__ __forceinline__ void decode_v3_body(const DecodeArgs &a, const int G,
             if (reduce_g(tag)) { t++; break; }
         }
     } else if (role == R_D) {
-        // ---------------- D ----------------
+        // ---------------- D (+ lm_head) ----------------
         // rms_norm(X1) -> gate/up + bias -> SwiGLU -> ACT (nn.c:61-78,
         // simd.h:394-397); unit f = gate row f and up row f
+        auto load_d = [&](const LayerOff &w_, int j, int f) {
+            load_u(j, w_.wgu + 2 * (size_t)f * ldD, w_.bg + (size_t)f, w_.bu + (size_t)f);
+        };
         for (; t < a.n_steps; t++) {
             const unsigned tag = a.step0 + (unsigned)t;
             for (int l = 0; l < a.L; l++) {
                 TRACE_EV(l, 0);
                 const LayerOff w = load_layer(a.layers + l);
                 asm volatile("" : "+v"(lane));
-                auto load_d = [&](const LayerOff &w_, int j, int f) {
-                    load_u(j, w_.wgu + 2 * (size_t)f * ldD, w_.bg + (size_t)f, w_.bu + (size_t)f);
-                };
                 auto load_dw = [&](int j, int f) { load_d(w, j, f); };
-                if (l == 0) {
+                if (l == 0 && !pre) {
                     prefetch(F, nDD, load_dw);
                     load_gamma<DC>(gp, rw, w.g_ffn, lane);
                 }
+                pre = false;
                 stage_rows<NB * 6 / WPB + 1>(x1s, ldD, D, nrows, a.ex.x1(l, 0), xstride, xa, tag, wid, lane, wt);
                 __syncthreads();
                 TRACE_EV(l, 6);
@@ -742,7 +747,17 @@ __device__ __forceinline__ void decode_v3_body(const DecodeArgs &a, const int G,
                     const LayerOff wn = load_layer(a.layers + l + 1);
                     prefetch(F, nDD, [&](int j, int f) { load_d(wn, j, f); });
                     load_gamma<DC>(gp, rw, wn.g_ffn, lane);
+                } else {
+                    prefetch_f();
                 }
+            }
+            lm_head(tag);
+            {
+                // layer 0 of the next step, loaded while the partials are gathered
+                const LayerOff w0 = load_layer(a.layers);
+                prefetch(F, nDD, [&](int j, int f) { load_d(w0, j, f); });
+                load_gamma<DC>(gp, rw, w0.g_ffn, lane);
+                pre = true;
             }
             if (reduce_g(tag)) { t++; break; }
         }
