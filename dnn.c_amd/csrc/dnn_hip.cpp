@@ -558,6 +558,13 @@ int decode_launch(dnn_hip_session *s, const int *feed, int n_feed_all, const int
     Roles roles{};
     if (!plan_roles(grid, m->D, m->F, m->ldD, m->ldF, B * m->H * a.ex.ns, roles))
         return fail(DNN_HIP_EINVAL, "a grid of %d workgroups is too small for the decode kernel's roles", grid);
+    if (const char *e = getenv("DNN_HIP_ROLES")) {     // "n_ac,n_d,n_e": a fixed split (tuning)
+        Roles r{};
+        if (sscanf(e, "%d,%d,%d", &r.n_ac, &r.n_d, &r.n_e) != 3 || r.n_ac < 1 || r.n_d < 1 || r.n_e < 1 ||
+            r.n_ac + r.n_d + r.n_e >= grid)
+            return fail(DNN_HIP_EINVAL, "DNN_HIP_ROLES=%s: needs n_ac,n_d,n_e >= 1 with a sum below the grid %d", e, grid);
+        roles = r;
+    }
     a.n_ac = roles.n_ac; a.n_d = roles.n_d; a.n_e = roles.n_e;
     s->next_tag += (unsigned)n_steps;
     void *kargs[] = {&a};
