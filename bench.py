@@ -98,13 +98,17 @@ def weight_floats(V, D, Ly, F):
     return V * D + Ly * per_layer + D + V
 
 
-def step_bytes(V, D, Ly, F, positions, B):
+def step_bytes(V, D, Ly, F, positions, B, bf16=False):
     """Algorithmic HBM bytes of the decode steps whose new tokens sit at
     `positions` (0-based, S = pos+1 cached keys attended): every weight once per
-    step, each row's K and V history read once per layer, one K and V row
-    written.  `positions` holds one position per step for B rows at the same
-    position, or (per-row lengths) one list of B positions per step."""
+    step (the matrices at 2 bytes each for bf16 weights), each row's K and V
+    history read once per layer, one K and V row written.  `positions` holds one
+    position per step for B rows at the same position, or (per-row lengths) one
+    list of B positions per step."""
     w = 4 * weight_floats(V, D, Ly, F)
+    if bf16:
+        mats = V * D + Ly * (3 * D * D + D * D + 3 * D * F)
+        w -= 2 * mats
     total = 0
     for p in positions:
         rows = list(p) if hasattr(p, "__len__") else [p] * B
@@ -212,12 +216,17 @@ def cpu_baseline_batched(cfg, B, prompt, new_tokens):
             "host": host_identity()}
 
 
-def decode_run(L, cfg, steps, warmup, grid=0):
+def decode_run(L, cfg, steps, warmup, grid=0, bf16=False):
     """Greedy decode of CONFIGS[cfg]: prompt, warmup, then exactly `steps` timed
-    steps in one dnn_hip_decode call.  Returns the measurement dict."""
+    steps in one dnn_hip_decode call (bf16: the same model with its weight
+    matrices stored as bf16, W16A32).  Returns the measurement dict."""
     V, D, Ly, H, F, P, B = CONFIGS[cfg]
     max_seq = P + warmup + steps + 1
     ctx, lm, dm = build_model(L, cfg, max(max_seq, 1088))
+    if bf16:
+        L.decoder_lm_device_model_ex.argtypes = [C.c_void_p, C.c_int]
+        L.decoder_lm_device_model_ex.restype = C.c_void_p
+        dm = DeviceModel(L.decoder_lm_device_model_ex(lm, dnn_amd.WEIGHTS_BF16), V, D)
     s = dnn_amd.HipSession(dm, B, max_seq)
     if grid:
         s.set_grid(grid)
@@ -232,7 +241,7 @@ def decode_run(L, cfg, steps, warmup, grid=0):
     dev_ms = s.last_ms()
     assert ids.shape[0] == steps
     positions = range(start_pos, start_pos + steps)
-    nbytes = step_bytes(V, D, Ly, F, positions, B)
+    nbytes = step_bytes(V, D, Ly, F, positions, B, bf16)
     achieved = nbytes / (dev_ms * 1e-3) / 1e9
     kern = s.kernel()
     return {
@@ -433,7 +442,8 @@ def main():
                          "known size, the scale for rocprofv3 FETCH_SIZE / WRITE_SIZE counters)")
     ap.add_argument("--cpu-tokens", type=int, default=24)
     ap.add_argument("--no-cpu-baseline", action="store_true")
-    ap.add_argument("--no-extra", action="store_true", help="the headline workload only (no C3 line)")
+    ap.add_argument("--no-extra", action="store_true", help="the headline workload only (no C3 / bf16 lines)")
+    ap.add_argument("--bf16", action="store_true", help="the decode workload with bf16 weight matrices (W16A32)")
     args = ap.parse_args()
     if args.gpus != 1:
         print("bench.py: this build runs on one GPU only (one-GPU boxes); --gpus %d is not supported" % args.gpus,
@@ -450,7 +460,7 @@ def main():
     elif cfg == "c5":
         r = run_c5(L, args)
     else:
-        r = decode_run(L, cfg, args.steps, args.warmup, args.grid)
+        r = decode_run(L, cfg, args.steps, args.warmup, args.grid, bf16=args.bf16)
     V, D, Ly, H, F, P, B = CONFIGS[cfg]
     steps = len(range(r["positions"][0], r["positions"][1] + 1)) if cfg not in ("c5",) else (
         args.steps if args.steps != 512 else 16)
@@ -465,7 +475,7 @@ def main():
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "bf16 weights / f32" if cfg == "c5" else "f32",
+        "dtype": "bf16 weights / f32" if cfg == "c5" or args.bf16 else "f32",
         "data": "synthetic: seeded N(0,0.02) weights, uniform-random prompt" + (
             ", N(0,1) patch embeddings" if cfg == "c5" else ""),
         "config": {"workload": r.get("workload", "%s greedy decode, batch %d" % (cfg.upper(), r["B"])),
@@ -479,7 +489,7 @@ def main():
     if "prefill" in r:
         line["prefill"] = r["prefill"]
     positions = range(r["positions"][0], r["positions"][1] + 1)
-    traffic, prof = measured_traffic(cfg, positions) if cfg not in ("c4", "c5") else (None, None)
+    traffic, prof = measured_traffic(cfg, positions) if cfg not in ("c4", "c5") and not args.bf16 else (None, None)
     line["roofline"]["traffic"] = traffic
     if prof is not None:
         line["roofline"]["traffic_profiled_launch"] = prof
@@ -490,6 +500,15 @@ def main():
         line["c3_batch32"]["workload"] = r3["workload"]
         if not args.no_cpu_baseline:
             line["c3_batch32"]["cpu_baseline"] = cpu_baseline_batched("c3", 32, 16, 8)
+        # the bf16-weight variant of the headline (north_star: reported
+        # separately, with its tolerance)
+        rb = decode_run(L, cfg, args.steps, args.warmup, args.grid, bf16=True)
+        line["c2_bf16"] = summary(rb)
+        line["c2_bf16"]["workload"] = "C2 greedy decode, batch 1, weight matrices stored as bf16 (W16A32)"
+        line["c2_bf16"]["dtype"] = "bf16 weights / f32"
+        line["c2_bf16"]["tolerance"] = ("against fp32 arithmetic on the bf16-rounded weights: logits max-abs 1e-3 "
+                                        "and relative 1e-4, greedy tokens identical "
+                                        "(tests/test_configs_gpu.py::test_c2_bf16_weights_every_step_logits)")
     if args.copy_probe:
         copy_probe(args.copy_probe << 20)
     if not args.no_cpu_baseline and cfg in CONFIGS and cfg not in ("c3", "c4", "c5"):

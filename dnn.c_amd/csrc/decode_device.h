@@ -207,20 +207,42 @@ __device__ __forceinline__ void rms_lds(const float *xs, int ld, int n, float ep
     }
 }
 
-// weights of R consecutive out-major rows starting at float offset `off` in the
-// arena (row stride ld floats), DC chunks of 256 columns each
-template <int R, int DC>
-__device__ __forceinline__ void load_rows(f4 (&w)[R][DC], rsrc_t rw, size_t off, int ld, int lane) {
+// One lane's piece of a weight row chunk: 4 consecutive weights, fp32 (f4) or
+// bf16 (u2, element 0 in the low half of .x), widened to fp32 where used.
+template <bool BF> struct WPiece { typedef f4 T; };
+template <> struct WPiece<true> { typedef u2 T; };
+__device__ __forceinline__ f4 widen(f4 v) { return v; }
+__device__ __forceinline__ f4 widen(u2 v) {
+    f4 r;
+    r.x = as_float(v.x << 16); r.y = as_float(v.x & 0xffff0000u);
+    r.z = as_float(v.y << 16); r.w = as_float(v.y & 0xffff0000u);
+    return r;
+}
+// lane `lane`'s piece of the 256-column chunk starting at element `off`
+template <bool BF>
+__device__ __forceinline__ typename WPiece<BF>::T ld_piece(rsrc_t rm, size_t off, int lane) {
+    if constexpr (BF)
+        return __builtin_amdgcn_raw_buffer_load_b64(rm, (unsigned)((off + 4 * lane) * 2), 0, CP_NT);
+    else
+        return ld4<CP_NT>(rm, (off + 4 * lane) * 4);
+}
+
+// weights of R consecutive out-major rows starting at element `off` of the
+// matrix arena `rm` (fp32, or bf16 at the same element offsets; row stride ld
+// elements), DC chunks of 256 columns each
+template <int R, int DC, bool BF>
+__device__ __forceinline__ void load_rows(typename WPiece<BF>::T (&w)[R][DC], rsrc_t rm, size_t off, int ld, int lane) {
 #pragma unroll
     for (int r = 0; r < R; r++)
 #pragma unroll
-        for (int k = 0; k < DC; k++) w[r][k] = ld4<CP_NT>(rw, (off + (size_t)r * ld + k * 256 + 4 * lane) * 4);
+        for (int k = 0; k < DC; k++) w[r][k] = ld_piece<BF>(rm, off + (size_t)r * ld + k * 256, lane);
 }
 
-// Per-lane partial sums of dot_lds, before the wavefront reduction:
-// s[r * NB + b] = this lane's share of w[r] . y_b.
-template <int R, int NB, int DC, bool NORM>
-__device__ __forceinline__ void part_lds(const f4 (&w)[R][DC], const float *xs, int ld, const float (&rs)[NB],
+// Per-lane partial sums of the row dot products, before the wavefront
+// reduction: s[r * NB + b] = this lane's share of w[r] . y_b, y_b = LDS row b,
+// optionally normalised as (x * rs) * gamma (norm.c:466-471) first.
+template <int R, int NB, int DC, bool NORM, typename WT>
+__device__ __forceinline__ void part_lds(const WT (&w)[R][DC], const float *xs, int ld, const float (&rs)[NB],
                                          const f4 (&g)[DC], int lane, float *s) {
 #pragma unroll
     for (int b = 0; b < NB; b++) {
@@ -234,8 +256,10 @@ __device__ __forceinline__ void part_lds(const f4 (&w)[R][DC], const float *xs, 
                 y.z = (y.z * rs[b]) * g[k].z; y.w = (y.w * rs[b]) * g[k].w;
             }
 #pragma unroll
-            for (int r = 0; r < R; r++)
-                s[r * NB + b] += w[r][k].x * y.x + w[r][k].y * y.y + w[r][k].z * y.z + w[r][k].w * y.w;
+            for (int r = 0; r < R; r++) {
+                const f4 wv = widen(w[r][k]);
+                s[r * NB + b] += wv.x * y.x + wv.y * y.y + wv.z * y.z + wv.w * y.w;
+            }
         }
     }
 }
@@ -261,41 +285,17 @@ __device__ __forceinline__ void wave_sum_n(float *v) {
     for (int i = 0; i < N; i++) v[i] = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v[i]), 63));
 }
 
-// acc[r][b] = sum_k w[r][k] . y_b[k], y_b = LDS row b, optionally normalised
-// as (x * rs) * gamma (norm.c:466-471) before the product.
-template <int R, int NB, int DC, bool NORM>
-__device__ __forceinline__ void dot_lds(const f4 (&w)[R][DC], const float *xs, int ld, const float (&rs)[NB],
-                                        const f4 (&g)[DC], int lane, float (&acc)[R][NB]) {
-#pragma unroll
-    for (int b = 0; b < NB; b++) {
-        float s[R];
-#pragma unroll
-        for (int r = 0; r < R; r++) s[r] = 0.f;
-#pragma unroll
-        for (int k = 0; k < DC; k++) {
-            f4 y = *reinterpret_cast<const f4 *>(xs + b * ld + k * 256 + 4 * lane);
-            if (NORM) {
-                y.x = (y.x * rs[b]) * g[k].x; y.y = (y.y * rs[b]) * g[k].y;
-                y.z = (y.z * rs[b]) * g[k].z; y.w = (y.w * rs[b]) * g[k].w;
-            }
-#pragma unroll
-            for (int r = 0; r < R; r++) s[r] += w[r][k].x * y.x + w[r][k].y * y.y + w[r][k].z * y.z + w[r][k].w * y.w;
-        }
-#pragma unroll
-        for (int r = 0; r < R; r++) acc[r][b] = wave_sum(s[r]);
-    }
-}
-
-// R weight rows of one work unit and their biases, loaded together before the
-// unit's inputs are waited for.
-template <int R, int DC>
+// R weight rows of one work unit and their biases (fp32 arena), loaded
+// together ahead of the unit's phase.
+template <int R, int DC, bool BF = false>
 struct RowUnit {
-    f4 w[R][DC];
+    typename WPiece<BF>::T w[R][DC];
     float bias[R];
 };
-template <int R, int DC>
-__device__ __forceinline__ void load_unit(RowUnit<R, DC> &u, rsrc_t rw, size_t woff, int ld, const size_t (&boff)[R], int lane) {
-    load_rows<R, DC>(u.w, rw, woff, ld, lane);
+template <int R, int DC, bool BF>
+__device__ __forceinline__ void load_unit(RowUnit<R, DC, BF> &u, rsrc_t rw, rsrc_t rm, size_t woff, int ld,
+                                          const size_t (&boff)[R], int lane) {
+    load_rows<R, DC, BF>(u.w, rm, woff, ld, lane);
 #pragma unroll
     for (int r = 0; r < R; r++) u.bias[r] = ld1<0>(rw, boff[r] * 4);
 }

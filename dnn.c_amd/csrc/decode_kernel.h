@@ -88,6 +88,7 @@ struct DecodeArgs {
     int V, D, L, H, F, ldD, ldF;
     const float *wts;       // weight arena: embedding [V][ldD] (also the tied
     uint32_t wts_bytes;     // lm_head), lm_head bias, final gamma, the blocks
+    const uint16_t *wts16;  // bf16 copy of the arena's matrices (same element offsets), or null
     uint32_t embed, lm_bias, g_final;   // float offsets in the arena
     const LayerOff *layers; // [L], device
     float eps_final;
@@ -160,6 +161,6 @@ inline size_t lds_bytes(int nb, int ldD, int ldF) {
     return (size_t)4 * ((LDS_HEAD_WORDS + 3) / 4 * 4) + (size_t)4 * nb * (3 * (size_t)ldD + ldF);
 }
 
-const void *decode_kernel_for(int nb, int dc);
+const void *decode_kernel_for(int nb, int dc, bool bf16);
 
 }  // namespace dnnhip

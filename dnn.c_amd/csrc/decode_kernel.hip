@@ -126,7 +126,7 @@ __device__ __forceinline__ void stage_att_split(float *as, int ld, int nh, int H
 // workgroup r is (k * n_role + r) * WPB + wid, so a workgroup's outputs of a
 // round are contiguous; the first PH rounds stay in registers ahead of the
 // phase, later ones load in batches of PH.
-template <int NB, int DC>
+template <int NB, int DC, bool BF>
 __device__ __forceinline__ void decode_v3_body(const DecodeArgs &a, const int G, const int g0) {
     extern __shared__ float smem[];
     int *s_tok = reinterpret_cast<int *>(smem);                 // [MAXB]
@@ -155,6 +155,9 @@ __device__ __forceinline__ void decode_v3_body(const DecodeArgs &a, const int G,
 
     const size_t kv_head = (size_t)DK * a.max_seq;              // floats per (layer, row, head)
     const rsrc_t rw = buf(a.wts, a.wts_bytes);
+    // weight matrices: the fp32 arena, or its bf16 copy at the same element
+    // offsets (biases, gammas and the embedding gather always read the fp32 arena)
+    const rsrc_t rm = BF ? buf(a.wts16, a.wts_bytes / 2) : rw;
     const rsrc_t xa = buf(a.xa, a.ex.total(a.L) * 8);
     const size_t kv_bytes = ((size_t)a.L * B * H * kv_head + (size_t)CH * DK) * 4;   // incl. the padding
     const rsrc_t rk = buf(a.kc, kv_bytes);
@@ -210,12 +213,12 @@ __device__ __forceinline__ void decode_v3_body(const DecodeArgs &a, const int G,
     // GEMV units held ahead of their phase: rows (2u, 2u+1) of a [*, ldD]
     // matrix and their biases, or, for an A unit, also the RoPE factors of the
     // rows' positions (lane b < NB: row b)
-    RowUnit<2, DC> U[PH];
+    RowUnit<2, DC, BF> U[PH];
     float rc[PH], rsn[PH];
     f4 gp[DC];                                                   // gamma of the held phase
     auto load_u = [&](int j, size_t woff, size_t b0, size_t b1) {
         const size_t bo[2] = {b0, b1};
-        load_unit<2, DC>(U[j], rw, woff, ldD, bo, lane);
+        load_unit<2, DC, BF>(U[j], rw, rm, woff, ldD, bo, lane);
     };
     auto load_a = [&](int j, const LayerOff &w, int u, int dpos) {
         const int n = 2 * u;
@@ -765,13 +768,13 @@ __device__ __forceinline__ void decode_v3_body(const DecodeArgs &a, const int G,
         // ---------------- E (+ lm_head) ----------------
         // down + bias + residual -> X2 (transformer.c:415); unit n = row n,
         // PE rounds held in registers
-        f4 wr[PE][FCMAX];
+        typename WPiece<BF>::T wr[PE][FCMAX];
         float bdn[PE];
         const int FC = ldF / 256;
         auto load_e = [&](const LayerOff &w_, int j, int n) {
 #pragma unroll
             for (int c = 0; c < FCMAX; c++)
-                if (c < FC) wr[j][c] = ld4<CP_NT>(rw, (w_.wd + (size_t)n * ldF + c * 256 + 4 * lane) * 4);
+                if (c < FC) wr[j][c] = ld_piece<BF>(rm, w_.wd + (size_t)n * ldF + c * 256, lane);
             bdn[j] = ld1<0>(rw, (w_.bd + (size_t)n) * 4);
         };
         auto prefetch_e = [&](const LayerOff &w_) {
@@ -814,7 +817,8 @@ __device__ __forceinline__ void decode_v3_body(const DecodeArgs &a, const int G,
                             for (int c = 0; c < FCMAX; c++) {
                                 if (c >= FC) continue;
                                 const f4 y = *reinterpret_cast<const f4 *>(acts + b * ldF + c * 256 + 4 * lane);
-                                sum += wr[j][c].x * y.x + wr[j][c].y * y.y + wr[j][c].z * y.z + wr[j][c].w * y.w;
+                                const f4 wv = widen(wr[j][c]);
+                                sum += wv.x * y.x + wv.y * y.y + wv.z * y.z + wv.w * y.w;
                             }
                             sum = wave_sum(sum);
                             if (lane == 0) out[wid * NB + b] = x1s[b * ldD + n] + (sum + bdn[j]);
@@ -849,17 +853,21 @@ __device__ __forceinline__ void decode_v3_body(const DecodeArgs &a, const int G,
 }
 
 
-template <int NB, int DC>
+template <int NB, int DC, bool BF>
 __global__ void __launch_bounds__(BLOCK)
 decode_v3(DecodeArgs a) {
-    decode_v3_body<NB, DC>(a, gridDim.x, blockIdx.x);
+    decode_v3_body<NB, DC, BF>(a, gridDim.x, blockIdx.x);
 }
 
-#define DNNHIP_INST(NB, DC) template __global__ void decode_v3<NB, DC>(DecodeArgs);
-DNNHIP_INST(1, 1) DNNHIP_INST(1, 2) DNNHIP_INST(1, 3)
-DNNHIP_INST(2, 1) DNNHIP_INST(2, 2) DNNHIP_INST(2, 3)
-DNNHIP_INST(4, 1) DNNHIP_INST(4, 2) DNNHIP_INST(4, 3)
-DNNHIP_INST(8, 1) DNNHIP_INST(8, 2) DNNHIP_INST(8, 3)
+#define DNNHIP_INST(NB, DC, BF) template __global__ void decode_v3<NB, DC, BF>(DecodeArgs);
+DNNHIP_INST(1, 1, false) DNNHIP_INST(1, 2, false) DNNHIP_INST(1, 3, false)
+DNNHIP_INST(2, 1, false) DNNHIP_INST(2, 2, false) DNNHIP_INST(2, 3, false)
+DNNHIP_INST(4, 1, false) DNNHIP_INST(4, 2, false) DNNHIP_INST(4, 3, false)
+DNNHIP_INST(8, 1, false) DNNHIP_INST(8, 2, false) DNNHIP_INST(8, 3, false)
+// bf16 weights: 1-4 rows (more rows of a bf16 model run on the batched engine)
+DNNHIP_INST(1, 1, true) DNNHIP_INST(1, 2, true) DNNHIP_INST(1, 3, true)
+DNNHIP_INST(2, 1, true) DNNHIP_INST(2, 2, true) DNNHIP_INST(2, 3, true)
+DNNHIP_INST(4, 1, true) DNNHIP_INST(4, 2, true) DNNHIP_INST(4, 3, true)
 
 #ifdef DNNHIP_TRACE
 extern "C" int dnn_hip_trace_arm(int step) {
@@ -873,12 +881,16 @@ extern "C" int dnn_hip_trace_read(unsigned long long *out) {
 }
 #endif
 
-const void *decode_kernel_for(int nb, int dc) {
-#define DNNHIP_PICK(NB, DC) if (nb == NB && dc == DC) return reinterpret_cast<const void *>(&decode_v3<NB, DC>);
-    DNNHIP_PICK(1, 1) DNNHIP_PICK(1, 2) DNNHIP_PICK(1, 3)
-    DNNHIP_PICK(2, 1) DNNHIP_PICK(2, 2) DNNHIP_PICK(2, 3)
-    DNNHIP_PICK(4, 1) DNNHIP_PICK(4, 2) DNNHIP_PICK(4, 3)
-    DNNHIP_PICK(8, 1) DNNHIP_PICK(8, 2) DNNHIP_PICK(8, 3)
+const void *decode_kernel_for(int nb, int dc, bool bf16) {
+#define DNNHIP_PICK(NB, DC, BF) \
+    if (nb == NB && dc == DC && bf16 == BF) return reinterpret_cast<const void *>(&decode_v3<NB, DC, BF>);
+    DNNHIP_PICK(1, 1, false) DNNHIP_PICK(1, 2, false) DNNHIP_PICK(1, 3, false)
+    DNNHIP_PICK(2, 1, false) DNNHIP_PICK(2, 2, false) DNNHIP_PICK(2, 3, false)
+    DNNHIP_PICK(4, 1, false) DNNHIP_PICK(4, 2, false) DNNHIP_PICK(4, 3, false)
+    DNNHIP_PICK(8, 1, false) DNNHIP_PICK(8, 2, false) DNNHIP_PICK(8, 3, false)
+    DNNHIP_PICK(1, 1, true) DNNHIP_PICK(1, 2, true) DNNHIP_PICK(1, 3, true)
+    DNNHIP_PICK(2, 1, true) DNNHIP_PICK(2, 2, true) DNNHIP_PICK(2, 3, true)
+    DNNHIP_PICK(4, 1, true) DNNHIP_PICK(4, 2, true) DNNHIP_PICK(4, 3, true)
     return nullptr;
 }
 

@@ -94,7 +94,7 @@ int dnn_hip_decode_static(dnn_hip_model *m, int batch, int max_seq, float *kc, f
     const size_t kv_bytes = dnn_hip_kv_floats(m, batch, max_seq) * sizeof(float);
     if (kv_bytes >= 0x7fffffffu) return set_error(DNN_HIP_EINVAL, "KV cache of %zu bytes: must stay < 2 GiB", kv_bytes);
     const int nb = batch > 4 ? 8 : batch > 2 ? 4 : batch > 1 ? 2 : 1;
-    const void *kern = decode_kernel_for(nb, m->ldD / LDALIGN);
+    const void *kern = decode_kernel_for(nb, m->ldD / LDALIGN, false);
     const size_t shmem = lds_bytes(nb, m->ldD, m->ldF);
     if (!kern || shmem > (size_t)lds_max) return set_error(DNN_HIP_EINVAL, "no decode kernel for this shape");
     if (hipFuncSetAttribute(kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)shmem) != hipSuccess)

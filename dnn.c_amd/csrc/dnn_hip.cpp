@@ -293,10 +293,10 @@ int dnn_hip_session_create(dnn_hip_model *m, int B, int max_seq, dnn_hip_session
     if (const char *k = getenv("DNN_HIP_ATT_SPLITS")) s->att_splits_req = atoi(k);
     // the batched engine for more than 4 rows (from 5 rows on it beats the
     // persistent kernel, which runs 5-8 rows at its 8-row cost: C2 at 8 rows
-    // 17.8k vs 15.4k tokens/s, 1,024-key histories 14.5k vs 11.5k), bf16
-    // weights, or on request; DNN_HIP_DECODE_KERNEL=3 keeps up to 8 rows on
-    // the persistent kernel
-    s->batched = B > MAXB || m->bf16 || s->kernel_pref == 6 || (B > 4 && s->kernel_pref != 3);
+    // 17.8k vs 15.4k tokens/s, 1,024-key histories 14.5k vs 11.5k), or on
+    // request; DNN_HIP_DECODE_KERNEL=3 keeps up to 8 rows of an fp32 model on
+    // the persistent kernel (its bf16 form covers 1-4 rows)
+    s->batched = B > MAXB || s->kernel_pref == 6 || (B > 4 && (s->kernel_pref != 3 || m->bf16));
     int n_cu = 0;
     if (hipDeviceGetAttribute(&n_cu, hipDeviceAttributeMultiprocessorCount, m->device) != hipSuccess || n_cu <= 0) n_cu = 256;
     s->grid_cap = n_cu;
@@ -508,7 +508,7 @@ int decode_launch(dnn_hip_session *s, const int *feed, int n_feed_all, const int
     HIP_TRY(hipDeviceGetAttribute(&lds_max, hipDeviceAttributeMaxSharedMemoryPerBlock, m->device));
     int grid = s->grid_cap;
     if (s->grid_req > 0) grid = std::min(grid, s->grid_req);
-    const void *kern = decode_kernel_for(nb, dc);
+    const void *kern = decode_kernel_for(nb, dc, m->bf16 != 0);
     const size_t shmem = lds_bytes(nb, m->ldD, m->ldF);
     if (!kern) return fail(DNN_HIP_EINVAL, "d_model %d: the decode kernels cover d_model <= %d", m->D, 3 * LDALIGN);
     s->kernel_used = 3;
@@ -540,6 +540,7 @@ int decode_launch(dnn_hip_session *s, const int *feed, int n_feed_all, const int
     a.V = m->V; a.D = m->D; a.L = m->L; a.H = m->H; a.F = m->F; a.ldD = m->ldD; a.ldF = m->ldF;
     a.wts = reinterpret_cast<const float *>(m->arena);
     a.wts_bytes = (uint32_t)m->arena_bytes;
+    a.wts16 = m->bf16 ? m->arena16 : nullptr;
     a.embed = (uint32_t)(m->off.embed / sizeof(float));
     a.lm_bias = (uint32_t)(m->off.lm_bias / sizeof(float));
     a.g_final = (uint32_t)(m->off.g_final / sizeof(float));

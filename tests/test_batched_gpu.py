@@ -225,7 +225,7 @@ def test_bf16_weights_match_rounded_oracle(B):
     feed = rng.integers(0, 128, size=(6, B)).astype(np.int32)
     s = A.HipSession(hm, B, 64)
     ids, lg = s.decode(feed, 30, want_logits=True)
-    assert s.kernel() == 6
+    assert s.kernel() == (3 if B <= 4 else 6)      # the persistent kernel's bf16 form, or the engine
     for b in range(B):
         want, wlg = m.generate(feed[:, b], 25, eos=-1, want_logits=True)
         assert list(ids[5:, b]) == list(want[6:]), "row %d" % b
