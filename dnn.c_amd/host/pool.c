@@ -1,6 +1,11 @@
 /* pool.c -- bump pools and the three-pool context (reference src/pool.c:8-57,
- * src/context.c:5-35): same layout, same zero-fill / copy / no-fill semantics,
- * same fatal assert on exhaustion. */
+ * src/context.c:5-35): same zero-fill / copy / no-fill semantics, same fatal
+ * assert on exhaustion.  One deliberate difference: every allocation starts
+ * on an 8-byte boundary.  A plain bump pointer hands the structs allocated
+ * from a pool (module items, tensors) 4-byte-aligned memory after an
+ * odd-length float array -- a misaligned access UBSan reports (undefined
+ * behaviour, and a fault on strict-alignment targets); the cost is at most 4
+ * bytes per allocation. */
 #include "dnn/pool.h"
 #include "dnn/context.h"
 #include <assert.h>
@@ -28,14 +33,15 @@ size_t mem_pool_mark(mem_pool *pool) { return pool->offset; }
 void   mem_pool_release(mem_pool *pool, size_t mark) { pool->offset = mark; }
 
 void *_mem_pool_alloc_nz(mem_pool *pool, size_t bytes) {
-    assert(pool->offset + bytes <= pool->capacity && "_mem_pool_alloc_nz: out of memory");
-    void *p = pool->buffer + pool->offset;
-    pool->offset += bytes;
+    const size_t start = (pool->offset + 7) & ~(size_t)7;
+    assert(start + bytes <= pool->capacity && "_mem_pool_alloc_nz: out of memory");
+    void *p = pool->buffer + start;
+    pool->offset = start + bytes;
     return p;
 }
 
 void *_mem_pool_alloc(mem_pool *pool, size_t bytes, const void *src) {
-    assert(pool->offset + bytes <= pool->capacity && "_mem_pool_alloc: out of memory");
+    assert(((pool->offset + 7) & ~(size_t)7) + bytes <= pool->capacity && "_mem_pool_alloc: out of memory");
     void *p = _mem_pool_alloc_nz(pool, bytes);
     if (src) memcpy(p, src, bytes);
     else memset(p, 0, bytes);
