@@ -110,7 +110,6 @@ __device__ __forceinline__ void decode_v3_body(const DecodeArgs &a, const int G,
     float *as = xs + NB * ldD;                                  // [NB][ldD] attention output
     float *x1s = as + NB * ldD;                                 // [NB][ldD] X1 (raw)
     float *acts = x1s + NB * ldD;                               // [NB][ldF] SwiGLU output
-    constexpr int OUTS = WPB * 2 * MAXB;                        // floats of one round's output block
     constexpr int PH = NB >= 8 ? 1 : NB >= 4 ? 2 : PU;          // rounds held in registers (<= PU)
 
     const int tid = threadIdx.x;
@@ -176,7 +175,10 @@ __device__ __forceinline__ void decode_v3_body(const DecodeArgs &a, const int G,
     if (role == R_ATT && r0 >= B * H * ns && r0 != nAT - 1) return;
 
     auto nrounds = [&](int nu, int n) { return (nu + n * WPB - 1) / (n * WPB); };
-    auto unit = [&](int k, int n) { return (k * n + r0) * WPB + wid; };
+    // unit of round k (of kr) on this workgroup: its rounds are consecutive
+    // blocks, so all of a workgroup's outputs of a phase are one contiguous
+    // range and leave in one store per row instead of one per round
+    auto unit = [&](int k, int kr) { return (r0 * kr + k) * WPB + wid; };
 
     // GEMV units held ahead of their phase: rows (2u, 2u+1) of a [*, ldD]
     // matrix and their biases, or, for an A unit, also the RoPE factors of the
@@ -208,25 +210,27 @@ __device__ __forceinline__ void decode_v3_body(const DecodeArgs &a, const int G,
         const int kr = nrounds(nu, n);
 #pragma unroll
         for (int j = 0; j < PH; j++)
-            if (j < kr) load(j, min(unit(j, n), nu - 1));
+            if (j < kr) load(j, min(unit(j, kr), nu - 1));
     };
     // Every round of a GEMV phase of 2-row units: per-lane partial sums of
     // the held units (part), one interleaved reduction of all of them, the
-    // epilogues (epi) leave each round's outputs in its OUT block, and
-    // wavefront 0 writes them; the trailing barrier also keeps the other
-    // wavefronts' next loads behind those stores.
-    auto gemv = [&](int nu, int n, auto &&load, auto &&part, auto &&epi, auto &&emit, int tl, int te) {
+    // epilogues (epi) leave the outputs in OUT (rr outputs per unit, rounds
+    // consecutive), and wavefront 0 writes the batch's rounds as one block
+    // (emit(out, first unit, units)); the trailing barrier also keeps the
+    // other wavefronts' next loads behind those stores.
+    auto gemv = [&](int nu, int n, int rr, auto &&load, auto &&part, auto &&epi, auto &&emit, int tl, int te) {
         const int kr = nrounds(nu, n);
+        const int ostr = WPB * NB * rr;
         for (int k0 = 0; k0 < kr; k0 += PH) {
             if (k0 > 0) {
 #pragma unroll
                 for (int j = 0; j < PH; j++)
-                    if (k0 + j < kr) load(j, min(unit(k0 + j, n), nu - 1));
+                    if (k0 + j < kr) load(j, min(unit(k0 + j, kr), nu - 1));
             }
             float sm[PH * 2 * NB];
 #pragma unroll
             for (int j = 0; j < PH; j++) {
-                const int u = unit(k0 + j, n);
+                const int u = unit(k0 + j, kr);
                 if (k0 + j < kr && u < nu) {
                     part(j, sm + j * 2 * NB);
                 } else {
@@ -237,17 +241,13 @@ __device__ __forceinline__ void decode_v3_body(const DecodeArgs &a, const int G,
             wave_sum_n<PH * 2 * NB>(sm);
 #pragma unroll
             for (int j = 0; j < PH; j++) {
-                const int u = unit(k0 + j, n);
-                if (k0 + j < kr && u < nu) epi(j, u, sm + j * 2 * NB, s_out + j * OUTS);
+                const int u = unit(k0 + j, kr);
+                if (k0 + j < kr && u < nu) epi(j, u, sm + j * 2 * NB, s_out + j * ostr);
             }
             TRACE_EV(tl, te);
             lds_barrier();
             TRACE_EV(tl, te + 1);
-            if (wid == 0) {
-#pragma unroll
-                for (int j = 0; j < PH; j++)
-                    if (k0 + j < kr) emit(s_out + j * OUTS, ((k0 + j) * n + r0) * WPB);
-            }
+            if (wid == 0) emit(s_out, (r0 * kr + k0) * WPB, min(PH, kr - k0) * WPB);
             lds_barrier();
         }
     };
@@ -449,8 +449,8 @@ __device__ __forceinline__ void decode_v3_body(const DecodeArgs &a, const int G,
                             if (lane == 0) { out[wid * NB * 2 + b * 2] = v0; out[wid * NB * 2 + b * 2 + 1] = v1; }
                         }
                     };
-                    gemv(nuA, nAC, load_aw, part_a, epi_a, [&](const float *out, int u0) {
-                        write_block<2, NB>(out, xa, a.ex.q(l, 0), xstride, u0, nuA, B, tag, lane);
+                    gemv(nuA, nAC, 2, load_aw, part_a, epi_a, [&](const float *out, int u0, int nv) {
+                        write_block<2, NB, PH * WPB>(out, xa, a.ex.q(l, 0), xstride, u0, min(nuA, u0 + nv), B, tag, lane);
                     }, l, 9);
                 }
                 TRACE_EV(l, 2);
@@ -468,7 +468,7 @@ __device__ __forceinline__ void decode_v3_body(const DecodeArgs &a, const int G,
                     stage_att_split(as, ldD, B * H, H, ns, a.ex.ao(a.L, l), a.ex.aml(a.L, l), xa, tag, wid, lane, wt);
                 __syncthreads();
                 TRACE_EV(l, 4);
-                gemv(nuC, nAC, load_c, [&](int j, float *sj) {
+                gemv(nuC, nAC, 2, load_c, [&](int j, float *sj) {
                     float rs[NB];
                     part_lds<2, NB, DC, false>(U[j].w, as, ldD, rs, gp, lane, sj);
                 }, [&](int j, int u, const float *acc, float *out) {
@@ -479,8 +479,8 @@ __device__ __forceinline__ void decode_v3_body(const DecodeArgs &a, const int G,
                             for (int r = 0; r < 2; r++)
                                 out[wid * NB * 2 + b * 2 + r] = xs[b * ldD + 2 * u + r] + (acc[r * NB + b] + U[j].bias[r]);
                     }
-                }, [&](const float *out, int u0) {
-                    write_block<2, NB>(out, xa, a.ex.x1(l, 0), xstride, u0, nuC, B, tag, lane);
+                }, [&](const float *out, int u0, int nv) {
+                    write_block<2, NB, PH * WPB>(out, xa, a.ex.x1(l, 0), xstride, u0, min(nuC, u0 + nv), B, tag, lane);
                 }, l, 11);
                 TRACE_EV(l, 5);
                 // the next layer's first A rounds (after the last layer: layer 0
@@ -700,7 +700,7 @@ __device__ __forceinline__ void decode_v3_body(const DecodeArgs &a, const int G,
                 float rs[NB];
                 rms_lds<NB, DC>(x1s, ldD, D, w.eps_ffn, lane, rs);
                 TRACE_EV(l, 12);
-                gemv(F, nDD, load_dw, [&](int j, float *sj) {
+                gemv(F, nDD, 1, load_dw, [&](int j, float *sj) {
                     part_lds<2, NB, DC, true>(U[j].w, x1s, ldD, rs, gp, lane, sj);
                 }, [&](int j, int f, const float *acc, float *out) {
                     if (lane == 0) {
@@ -710,8 +710,8 @@ __device__ __forceinline__ void decode_v3_body(const DecodeArgs &a, const int G,
                             out[wid * NB + b] = (gg / (1.0f + expf(-gg))) * up;
                         }
                     }
-                }, [&](const float *out, int u0) {
-                    write_block<1, NB>(out, xa, a.ex.act(l, 0), xstride, u0, F, B, tag, lane);
+                }, [&](const float *out, int u0, int nv) {
+                    write_block<1, NB, PH * WPB>(out, xa, a.ex.act(l, 0), xstride, u0, min(F, u0 + nv), B, tag, lane);
                 }, l, 14);
                 TRACE_EV(l, 7);
                 if (l + 1 < a.L) {
@@ -749,7 +749,7 @@ __device__ __forceinline__ void decode_v3_body(const DecodeArgs &a, const int G,
             const int kr = nrounds(D, nEE);
 #pragma unroll
             for (int j = 0; j < PE; j++)
-                if (j < kr) load_e(w_, j, min(unit(j, nEE), D - 1));
+                if (j < kr) load_e(w_, j, min(unit(j, kr), D - 1));
         };
         bool pre_e = false;                 // layer 0's rows held
         constexpr bool EF_EARLY = NB <= 2;
@@ -771,13 +771,13 @@ __device__ __forceinline__ void decode_v3_body(const DecodeArgs &a, const int G,
                     if (k0 > 0) {
 #pragma unroll
                         for (int j = 0; j < PE; j++)
-                            if (k0 + j < kr) load_e(w, j, min(unit(k0 + j, nEE), D - 1));
+                            if (k0 + j < kr) load_e(w, j, min(unit(k0 + j, kr), D - 1));
                     }
 #pragma unroll
                     for (int j = 0; j < PE; j++) {
-                        const int n = unit(k0 + j, nEE);
+                        const int n = unit(k0 + j, kr);
                         if (k0 + j >= kr || n >= D) continue;
-                        float *out = s_out + j * OUTS;
+                        float *out = s_out + j * (WPB * NB);
 #pragma unroll
                         for (int b = 0; b < NB; b++) {
                             float sum = 0.f;
@@ -796,11 +796,9 @@ __device__ __forceinline__ void decode_v3_body(const DecodeArgs &a, const int G,
                     lds_barrier();
                     TRACE_EV(l, 15);
                     if (wid == 0) {
-#pragma unroll
-                        for (int j = 0; j < PE; j++)
-                            if (k0 + j < kr)
-                                write_block<1, NB>(s_out + j * OUTS, xa, a.ex.x2(l, 0), xstride,
-                                                   ((k0 + j) * nEE + r0) * WPB, D, B, tag, lane);
+                        const int u0 = (r0 * kr + k0) * WPB;
+                        write_block<1, NB, PE * WPB>(s_out, xa, a.ex.x2(l, 0), xstride, u0,
+                                                     min(D, u0 + min(PE, kr - k0) * WPB), B, tag, lane);
                     }
                     lds_barrier();
                 }
