@@ -380,8 +380,8 @@ __device__ __forceinline__ void decode_v3_body(const DecodeArgs &a, const int G,
                 if (vv > v || (vv == v && ii < i)) { v = vv; i = ii; }
             }
             const size_t pa = a.ex.amax(a.L, t & 1, tid, fi);
-            put(xa, pa, v, tag);
-            put(xa, pa + 1, __builtin_bit_cast(float, i), tag);
+            const u4 rec = {as_uint(v), tag, (unsigned)i, tag};      // (value, index) pairs in one store
+            __builtin_amdgcn_raw_buffer_store_b128(rec, xa, (unsigned)(pa * 8), 0, CP_SC1);
         }
     };
     auto prefetch_f = [&]() {
@@ -648,7 +648,7 @@ __device__ __forceinline__ void decode_v3_body(const DecodeArgs &a, const int G,
                     s_part[wid * (DK + 2) + lane] = o_run;
                     if (lane == 0) { s_part[wid * (DK + 2) + DK] = m_run; s_part[wid * (DK + 2) + DK + 1] = l_run; }
                     TRACE_EV(l, 10);
-                    __syncthreads();
+                    lds_barrier();          // the cache appends complete at the record's closing barrier
                     TRACE_EV(l, 11);
                     if (wid == 0) {
                         // lanes w < WPB: wavefront w's weight e^(m_w - M)
