@@ -66,18 +66,6 @@ __device__ __forceinline__ float wave_sum(float v) {
     v += dpp<0x143, 0xc>(v, 0.f);     // row_bcast:31 into rows 2, 3
     return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 63));
 }
-// Two independent sums, their DPP steps interleaved (each hides the other's
-// DPP hazard wait states); same order of additions as wave_sum.
-__device__ __forceinline__ void wave_sum2(float &a, float &b) {
-    a += dpp<0xb1, 0xf>(a, 0.f);  b += dpp<0xb1, 0xf>(b, 0.f);
-    a += dpp<0x4e, 0xf>(a, 0.f);  b += dpp<0x4e, 0xf>(b, 0.f);
-    a += dpp<0x141, 0xf>(a, 0.f); b += dpp<0x141, 0xf>(b, 0.f);
-    a += dpp<0x140, 0xf>(a, 0.f); b += dpp<0x140, 0xf>(b, 0.f);
-    a += dpp<0x142, 0xa>(a, 0.f); b += dpp<0x142, 0xa>(b, 0.f);
-    a += dpp<0x143, 0xc>(a, 0.f); b += dpp<0x143, 0xc>(b, 0.f);
-    a = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, a), 63));
-    b = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, b), 63));
-}
 __device__ __forceinline__ float wave_max(float v) {
     v = fmaxf(v, dpp<0xb1, 0xf>(v, -INFINITY));
     v = fmaxf(v, dpp<0x4e, 0xf>(v, -INFINITY));
@@ -153,41 +141,6 @@ __device__ __forceinline__ void stage_rows(float *dst, int ld, int n, int nrows,
             const int r = c / cpr, col = (c - r * cpr) * 128 + 2 * lane;
             if (col < n) dst[r * ld + col] = as_float(q[i].x);
             if (col + 1 < n) dst[r * ld + col + 1] = as_float(q[i].z);
-        }
-    }
-}
-
-// Single-wavefront variant: one wavefront stages every chunk, in passes of up
-// to NCMAX chunks (a pass is polled until complete, then written to LDS).
-template <int NCMAX>
-__device__ __forceinline__ void stage_rows_1w(float *dst, int ld, int n, int nrows, size_t base0, size_t stride,
-                                              rsrc_t xa, unsigned tag, int lane, Waiter &wt) {
-    const int cpr = (n + 127) / 128, total = nrows * cpr;
-    for (int c0 = 0; c0 < total; c0 += NCMAX) {
-        u4 q[NCMAX];
-        wt.reset();
-        for (;;) {
-            bool ok = true;
-            // branch-free: chunks past the end re-read the last one, so every
-            // load of a pass is issued before the first wait
-#pragma unroll
-            for (int i = 0; i < NCMAX; i++) {
-                const int c = min(c0 + i, total - 1);
-                const int r = c / cpr, col = (c - r * cpr) * 128 + 2 * lane;
-                q[i] = __builtin_amdgcn_raw_buffer_load_b128(xa, (unsigned)((base0 + r * stride + col) * 8), 0, CP_SC1);
-                const unsigned t0 = q[i].y, t1 = q[i].w;
-                ok &= (col >= n || t0 == tag) && (col + 1 >= n || t1 == tag);
-            }
-            if (__all(ok) || !wt.again()) break;
-        }
-#pragma unroll
-        for (int i = 0; i < NCMAX; i++) {
-            const int c = c0 + i;
-            if (c < total) {
-                const int r = c / cpr, col = (c - r * cpr) * 128 + 2 * lane;
-                if (col < n) dst[r * ld + col] = as_float(q[i].x);
-                if (col + 1 < n) dst[r * ld + col + 1] = as_float(q[i].z);
-            }
         }
     }
 }
