@@ -19,6 +19,10 @@ constexpr int PU = 4;             // GEMV rounds of 2-row units a wavefront hold
 constexpr int PE = 2;             // down-projection rounds (rows of d_ffn) held ahead
 constexpr int CPW = 2;            // attention chunks a wavefront loads per pass
 
+// GEMV rounds a wavefront holds in registers ahead of a phase, for nb batch
+// rows and dc 256-column chunks per row (more rows: fewer held without spills)
+constexpr int hold_rounds(int nb, int dc) { return nb >= 8 ? (dc >= 3 ? 1 : 2) : nb >= 4 ? 2 : PU; }
+
 // Workgroup roles of the persistent decode kernel (see plan_roles)
 enum { R_AC = 0, R_ATT = 1, R_D = 2, R_E = 3 };
 
@@ -114,14 +118,16 @@ struct DecodeArgs {
 
 // Split of a grid of G workgroups into the kernel's roles: n_ac run the QKV
 // and out_proj GEMVs, n_d gate/up, n_e down, and the rest (at least
-// min(att_records, G / 5), at least 1) attention.  Among the splits that fit,
-// the one whose largest per-wavefront weight share of a phase (rounds x unit
-// length) is smallest, then the fewest rounds in total, then the most
-// workgroups.  Returns false when G cannot hold one workgroup per role.
+// min(att_records, G / 5), at least 1) attention.  Among the splits that fit
+// -- with every phase's rounds within what a wavefront holds in registers
+// (hold; PE for the down rows) where any split allows that -- the one whose
+// largest per-wavefront weight share of a phase (rounds x unit length) is
+// smallest, then the fewest rounds in total, then the most workgroups.
+// Returns false when G cannot hold one workgroup per role.
 struct Roles {
     int n_ac, n_d, n_e;
 };
-inline bool plan_roles(int G, int D, int F, int ldD, int ldF, int att_records, Roles &out) {
+inline bool plan_roles(int G, int D, int F, int ldD, int ldF, int att_records, Roles &out, int hold = PU) {
     const int n_att = att_records < G / 5 ? (att_records > 1 ? att_records : 1) : (G / 5 > 1 ? G / 5 : 1);
     const int R = G - n_att;
     if (R < 3) return false;
@@ -129,6 +135,7 @@ inline bool plan_roles(int G, int D, int F, int ldD, int ldF, int att_records, R
     auto cdiv = [](long x, long y) { return (int)((x + y - 1) / y); };
     long best_cost = -1;
     int best_rounds = 0, best_used = 0;
+    bool best_held = false;
     for (int ra = 1; ra <= 16; ra++)
         for (int rd = 1; rd <= 32; rd++)
             for (int re = 1; re <= 16; re++) {
@@ -141,10 +148,13 @@ inline bool plan_roles(int G, int D, int F, int ldD, int ldF, int att_records, R
                 if ((long)rd * 2 * ldD > cost) cost = (long)rd * 2 * ldD;
                 if ((long)re * ldF > cost) cost = (long)re * ldF;
                 const int rounds = ra + rc + rd + re;
-                const bool better = best_cost < 0 || cost < best_cost ||
-                                    (cost == best_cost && (rounds < best_rounds || (rounds == best_rounds && used > best_used)));
+                const bool held = ra <= hold && rc <= hold && rd <= hold && re <= PE;
+                const bool better = best_cost < 0 || (held && !best_held) ||
+                                    (held == best_held &&
+                                     (cost < best_cost ||
+                                      (cost == best_cost && (rounds < best_rounds || (rounds == best_rounds && used > best_used)))));
                 if (better) {
-                    best_cost = cost; best_rounds = rounds; best_used = used;
+                    best_cost = cost; best_rounds = rounds; best_used = used; best_held = held;
                     out = Roles{nac, nd, ne};
                 }
             }

@@ -110,7 +110,7 @@ __device__ __forceinline__ void decode_v3_body(const DecodeArgs &a, const int G,
     float *as = xs + NB * ldD;                                  // [NB][ldD] attention output
     float *x1s = as + NB * ldD;                                 // [NB][ldD] X1 (raw)
     float *acts = x1s + NB * ldD;                               // [NB][ldF] SwiGLU output
-    constexpr int PH = NB >= 8 ? 1 : NB >= 4 ? 2 : PU;          // rounds held in registers (<= PU)
+    constexpr int PH = hold_rounds(NB, DC);                     // rounds held in registers (<= PU)
 
     const int tid = threadIdx.x;
     int lane = tid & (WAVE - 1);

@@ -122,7 +122,7 @@ int dnn_hip_decode_static(dnn_hip_model *m, int batch, int max_seq, float *kc, f
     a.err = status; a.steps_done = status + 1;
     a.seq_limit = max_len;
     Roles roles{};
-    if (!plan_roles(n_cu, m->D, m->F, m->ldD, m->ldF, batch * m->H * a.ex.ns, roles))
+    if (!plan_roles(n_cu, m->D, m->F, m->ldD, m->ldF, batch * m->H * a.ex.ns, roles, hold_rounds(nb, m->ldD / LDALIGN)))
         return set_error(DNN_HIP_EINVAL, "a grid of %d workgroups is too small for the decode kernel's roles", n_cu);
     a.n_ac = roles.n_ac; a.n_d = roles.n_d; a.n_e = roles.n_e;
     {

@@ -557,7 +557,7 @@ int decode_launch(dnn_hip_session *s, const int *feed, int n_feed_all, const int
     a.n_steps = n_steps; a.eos = eos; a.step0 = s->next_tag; a.err = s->err; a.steps_done = s->steps_done;
     a.seq_limit = m->rope ? std::min(s->max_seq, m->rope_rows) : s->max_seq;
     Roles roles{};
-    if (!plan_roles(grid, m->D, m->F, m->ldD, m->ldF, B * m->H * a.ex.ns, roles))
+    if (!plan_roles(grid, m->D, m->F, m->ldD, m->ldF, B * m->H * a.ex.ns, roles, hold_rounds(nb, m->ldD / LDALIGN)))
         return fail(DNN_HIP_EINVAL, "a grid of %d workgroups is too small for the decode kernel's roles", grid);
     if (const char *e = getenv("DNN_HIP_ROLES")) {     // "n_ac,n_d,n_e": a fixed split (tuning)
         Roles r{};
