@@ -14,8 +14,17 @@
 //     E  down GEMV + bias + residual                          -> X2
 //   then
 //     F  rms_norm(X2) -> tied lm_head GEMV + bias -> argmax partial per workgroup
-//     G  every workgroup reduces the partials (first index of the maximum,
-//        gpt.c:220-230) and feeds the token to the next step's embedding rows
+//     G  one workgroup reduces the partials (first index of the maximum,
+//        gpt.c:220-230) and publishes the token, which feeds the next step's
+//        embedding rows
+//
+// Workgroups have roles for the whole launch (A+C, attention, D with a share
+// of F, E with a share of F) and each runs its own copy of the step/layer
+// loop, so no workgroup runs two consecutive phases: a workgroup stores its
+// outputs, then issues the weight loads of its next phase, which land while
+// the other roles work (a CU serves its vector-memory requests in order, so
+// loads issued between a workgroup's compute and its next wait would delay
+// either its stores or that wait).
 //
 // Synchronisation is dataflow, not grid barriers.  Every value a wavefront
 // produces for other workgroups is one 8-byte (value, tag) store with
@@ -25,16 +34,14 @@
 // step's tag, write it to LDS, and meet at a workgroup barrier.  Each
 // dependency costs one coherent hop, no L2 writeback/invalidate is issued, and
 // the row crosses the fabric once per workgroup rather than once per wavefront.
-// A wavefront issues the weight loads of its work unit before the staging
-// poll, so weight streaming overlaps the wait.
 //
 // Weights are out-major (row n = the K inputs of output n, padded to a multiple
 // of 256 floats): each output is one contiguous, coalesced dot product owned by
-// one wavefront; unit u of a phase goes to wavefront u mod (8 * grid), counted
-// workgroup-fastest, so consecutive units land on different CUs.  Every global
-// access goes through a buffer descriptor sized to its tensor, so the hardware
-// range-checks it (out-of-range loads read 0, stores are dropped).
-
+// one wavefront; a workgroup's units of a phase are consecutive, so its outputs
+// leave as one block.  Every global access goes through a buffer descriptor
+// sized to its tensor, so the hardware range-checks it (out-of-range loads
+// read 0, stores are dropped).  This file holds the fp32-weight instantiations
+// and the kernel lookup; the body is decode_kernel_body.h.
 
 #include "decode_kernel_body.h"
 
