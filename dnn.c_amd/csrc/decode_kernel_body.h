@@ -327,7 +327,7 @@ __device__ __forceinline__ void decode_v3_body(const DecodeArgs &a, const int G,
         for (int b = 0; b < NB; b++) { bv[b] = -INFINITY; bi[b] = 0x7fffffff; }
         const int nu = V / 2;
         stage_rows<NB * 6 / WPB + 1>(xs, ldD, D, nrows, a.ex.x2(a.L - 1, 0), xstride, xa, tag, wid, lane, wt);
-        __syncthreads();
+        lds_barrier();
         TRACE_EV(a.L, 1);
         float rs[NB];
         rms_lds<NB, DC>(xs, ldD, D, a.eps_final, lane, rs);
@@ -428,7 +428,7 @@ __device__ __forceinline__ void decode_v3_body(const DecodeArgs &a, const int G,
                 } else {
                     stage_rows<NB * 6 / WPB + 1>(xs, ldD, D, nrows, a.ex.x2(l - 1, 0), xstride, xa, tag, wid, lane, wt);
                 }
-                __syncthreads();
+                lds_barrier();
                 TRACE_EV(l, 1);
                 {
                     float rs[NB];
@@ -466,7 +466,7 @@ __device__ __forceinline__ void decode_v3_body(const DecodeArgs &a, const int G,
                     stage_rows<NB * 6 / WPB + 1>(as, ldD, D, nrows, a.ex.att(l, 0), xstride, xa, tag, wid, lane, wt);
                 else
                     stage_att_split(as, ldD, B * H, H, ns, a.ex.ao(a.L, l), a.ex.aml(a.L, l), xa, tag, wid, lane, wt);
-                __syncthreads();
+                lds_barrier();
                 TRACE_EV(l, 4);
                 gemv(nuC, nAC, 2, load_c, [&](int j, float *sj) {
                     float rs[NB];
@@ -695,7 +695,7 @@ __device__ __forceinline__ void decode_v3_body(const DecodeArgs &a, const int G,
                 }
                 pre = false;
                 stage_rows<NB * 6 / WPB + 1>(x1s, ldD, D, nrows, a.ex.x1(l, 0), xstride, xa, tag, wid, lane, wt);
-                __syncthreads();
+                lds_barrier();
                 TRACE_EV(l, 6);
                 float rs[NB];
                 rms_lds<NB, DC>(x1s, ldD, D, w.eps_ffn, lane, rs);
@@ -764,7 +764,7 @@ __device__ __forceinline__ void decode_v3_body(const DecodeArgs &a, const int G,
                 pre_e = false;
                 stage_rows<NB * 6 / WPB + 1>(x1s, ldD, D, nrows, a.ex.x1(l, 0), xstride, xa, tag, wid, lane, wt);
                 stage_rows<NB * 16 / WPB + 1>(acts, ldF, F, nrows, a.ex.act(l, 0), xstride, xa, tag, wid, lane, wt);
-                __syncthreads();
+                lds_barrier();
                 TRACE_EV(l, 8);
                 const int kr = nrounds(D, nEE);
                 for (int k0 = 0; k0 < kr; k0 += PE) {
