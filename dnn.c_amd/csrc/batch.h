@@ -83,6 +83,7 @@ struct GemmArgs {
     // HEAD
     uint2 *amax;                // [M][column tiles] (value bits, index) per lm_head tile
     unsigned *head_cnt;         // last-arriver counter of head_finish_kernel
+    uint2 *fin;                 // [BK_MAXM] tagged stop flags of head_finish_kernel's rows
     int amax_tiles;             // column tiles of the lm_head GEMM (partials per row)
     float *logits;              // [steps][M][V] or null
     int *ids;                   // [steps][M]

@@ -220,7 +220,7 @@ int engine_get(dnn_hip_session *s, int rows, int layout = 0) {
         const int ntn_head = (m->V + 15) / 16;
         e->part_pairs = engine_part_pairs(m);
         e->apart_pairs = (size_t)MAX_ROWS * m->H * 8 * (BK_DK + 2);
-        e->amax_pairs = (size_t)MAX_ROWS * ntn_head;
+        e->amax_pairs = (size_t)MAX_ROWS * ntn_head + BK_MAXM;      // partials, then the finisher's stop records
         int rc = 0;
         rc = rc ? rc : dalloc(&e->part, e->part_pairs);
         rc = rc ? rc : dalloc(&e->apart, e->apart_pairs);
@@ -402,6 +402,7 @@ int enqueue_head(dnn_hip_session *s, const PrefillPlan *pp, float *logits, int *
     g.bias = W.f(lm_bias);
     g.gamma = norm ? W.f(g_final) : nullptr; g.eps = m->eps_final; g.dnorm = m->D;
     g.amax = e->amax; g.head_cnt = e->cnt + CNT_GEMM + CNT_ATT;
+    g.fin = e->amax + (size_t)MAX_ROWS * ((m->V + 15) / 16);
     g.logits = logits; g.ids = ids;
     g.feed = s->feed; g.n_feed = s->n_feed; g.pos = s->pos;
     g.x_next = e->X; g.ldx = m->ldD; g.embed = W.f(embed);

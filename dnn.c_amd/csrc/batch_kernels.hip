@@ -491,133 +491,104 @@ __global__ __launch_bounds__(64 * WM * WN * KW) void gemm_kernel(const GemmArgs 
 }
 
 // The lm_head's argmax over its column tiles (gpt.c:220-230: the first index of
-// the maximum), then the step's bookkeeping: one workgroup of FIN_THR threads,
-// wavefront w taking rows w, w + 16, ...; the step state, each row's feed and
-// the tiles' partials are loaded together up front.
-constexpr int FIN_THR = 1024;
-constexpr int FIN_ROWS = BK_MAXM / (FIN_THR / 64);     // rows per wavefront
+// the maximum), then the step's bookkeeping: one workgroup per row.  A row's
+// partials, its feed and its state are loaded together up front, the next
+// step's embedding row as soon as the token is known; the last workgroup to
+// arrive (a counter) advances the step state.  Each row's stop flag reaches it
+// as a tagged record, so it needs no fence.
+constexpr int FIN_THR = 256;
+constexpr int FIN_SLOT = 127;          // tag slot of the stop records (the GEMMs use 0 .. 5 L)
 __global__ __launch_bounds__(FIN_THR) void head_finish_kernel(const GemmArgs g) {
-    __shared__ int s_all;
-    const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+    __shared__ float s_bv[FIN_THR / 64];
+    __shared__ int s_bi[FIN_THR / 64];
+    __shared__ int s_flag;
+    const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, m = blockIdx.x;
     BTRACE(g.st, g.kslot + 1, 0);
     const int done = __builtin_nontemporal_load(&g.st->done);
-    const int t = g.prefill ? 0 : g.st->t;
+    const bool dec = !g.prefill;
+    const int t = dec ? g.st->t : 0;
+    const unsigned tag = __builtin_nontemporal_load(&g.st->tag) * 128u + (unsigned)FIN_SLOT;
     const int ntn = g.amax_tiles;
-    if (tid == 0) s_all = g.eos >= 0;
-    // every row's inputs that do not depend on this step's token, loaded up
-    // front: prompt length, position, stop flag, and (once the step is known)
-    // the next prompt id
-    int nf[FIN_ROWS], ps[FIN_ROWS], rd[FIN_ROWS], fnext[FIN_ROWS];
-    float best[FIN_ROWS];
-    int bi[FIN_ROWS];
+    const int nf = dec ? g.n_feed[m] : 0, ps = dec ? g.pos[m] : 0, rd = dec ? g.row_done[m] : 0;
+    const int fnext = (dec && t + 1 < nf) ? g.feed[(size_t)(t + 1) * g.M + m] : -1;
+    // the partials in passes of FIN_PASS tiles per thread, every load of a pass
+    // issued before the first compare; tiles in increasing order per thread,
+    // strict '>' keeps the first maximum
+    constexpr int FIN_PASS = 4;
+    float best = -INFINITY;
+    int bi = 0x7fffffff;
+    for (int t0 = 0; t0 < ntn; t0 += FIN_THR * FIN_PASS) {
+        uint2 pv[FIN_PASS];
 #pragma unroll
-    for (int r = 0; r < FIN_ROWS; r++) {
-        best[r] = -INFINITY;
-        bi[r] = 0x7fffffff;
-        const int m = w + 16 * r;
-        const bool row = !g.prefill && m < g.M;
-        nf[r] = row ? g.n_feed[m] : 0;
-        ps[r] = row ? g.pos[m] : 0;
-        rd[r] = row ? g.row_done[m] : 0;
+        for (int j = 0; j < FIN_PASS; j++) {
+            const int tn = t0 + tid + FIN_THR * j;
+            pv[j] = tn < ntn ? g.amax[(size_t)m * ntn + tn] : make_uint2(as_uint(-INFINITY), 0x7fffffffu);
+        }
+#pragma unroll
+        for (int j = 0; j < FIN_PASS; j++) {
+            const float v = as_float(pv[j].x);
+            const int idx = (int)pv[j].y;
+            if (v > best || (v == best && idx < bi)) { best = v; bi = idx; }
+        }
     }
 #pragma unroll
-    for (int r = 0; r < FIN_ROWS; r++) {
-        const int m = w + 16 * r;
-        fnext[r] = (!g.prefill && m < g.M && t + 1 < nf[r]) ? g.feed[(size_t)(t + 1) * g.M + m] : -1;
+    for (int o = 32; o >= 1; o >>= 1) {
+        const float ov = __shfl_xor(best, o);
+        const int oi = __shfl_xor(bi, o);
+        if (ov > best || (ov == best && oi < bi)) { best = ov; bi = oi; }
     }
-    // the partials in passes of FIN_PASS tiles per lane, every load of a pass
-    // (all rows of the wavefront) issued before the first compare; tiles in
-    // increasing order per lane, strict '>' keeps the first maximum
-    constexpr int FIN_PASS = 8;
-    for (int t0 = 0; t0 < ntn; t0 += 64 * FIN_PASS) {
-        uint2 pv[FIN_ROWS][FIN_PASS];
-#pragma unroll
-        for (int r = 0; r < FIN_ROWS; r++)
-#pragma unroll
-            for (int j = 0; j < FIN_PASS; j++) {
-                const int m = w + 16 * r, tn = t0 + lane + 64 * j;
-                pv[r][j] = (m < g.M && tn < ntn) ? g.amax[(size_t)m * ntn + tn] : make_uint2(as_uint(-INFINITY), 0x7fffffffu);
-            }
-#pragma unroll
-        for (int r = 0; r < FIN_ROWS; r++)
-#pragma unroll
-            for (int j = 0; j < FIN_PASS; j++) {
-                const float v = as_float(pv[r][j].x);
-                const int idx = (int)pv[r][j].y;
-                if (v > best[r] || (v == best[r] && idx < bi[r])) { best[r] = v; bi[r] = idx; }
-            }
-    }
+    if (lane == 0) { s_bv[w] = best; s_bi[w] = bi; }
     BTRACE(g.st, g.kslot + 1, 2);
     if (done) return;
-    __syncthreads();                                   // s_all initialised
-    BTRACE(g.st, g.kslot + 1, 3);
-    // every row's token first, then every next-step embedding load, then the
-    // stores (a store could alias a later load: interleaved, each row's copy
-    // would wait for the previous row's)
-    int tokr[FIN_ROWS];
+    __syncthreads();
+    best = s_bv[0];
+    bi = s_bi[0];
 #pragma unroll
-    for (int r = 0; r < FIN_ROWS; r++) {
-        float bv = best[r];
-        int bx = bi[r];
-#pragma unroll
-        for (int o = 32; o >= 1; o >>= 1) {
-            const float ov = __shfl_xor(bv, o);
-            const int oi = __shfl_xor(bx, o);
-            if (ov > bv || (ov == bv && oi < bx)) { bv = ov; bx = oi; }
-        }
-        tokr[r] = bx == 0x7fffffff ? 0 : bx;
-    }
-    // four columns per lane and load: the arena's embedding rows are zero past
-    // D, so the last group may cover padding columns (X holds zeros there too)
-    constexpr int CPL = BK_MAXD / 256;
-    static_assert(BK_MAXD % 256 == 0, "whole float4 groups per lane");
-    float4 ev[FIN_ROWS][CPL];
-#pragma unroll
-    for (int r = 0; r < FIN_ROWS; r++) {
-        const int m = w + 16 * r;
-        const int nxt = fnext[r] >= 0 ? fnext[r] : tokr[r];
+    for (int k = 1; k < FIN_THR / 64; k++)
+        if (s_bv[k] > best || (s_bv[k] == best && s_bi[k] < bi)) { best = s_bv[k]; bi = s_bi[k]; }
+    const int tok = bi == 0x7fffffff ? 0 : bi;
+    const rsrc_t rf = buf(g.fin, (size_t)BK_MAXM * 8);
+    if (!dec) {
+        if (tid == 0) g.ids[m] = tok;
+    } else {
+        // the next step's embedding row (embedding.c:79-84); the arena's rows
+        // are zero past D, as X is
+        const int nxt = fnext >= 0 ? fnext : tok;
         const float4 *e = reinterpret_cast<const float4 *>(g.embed + (size_t)nxt * g.ldx);
-        const bool live = !g.prefill && m < g.M;
-#pragma unroll
-        for (int j = 0; j < CPL; j++)
-            ev[r][j] = (live && 4 * (lane + 64 * j) < g.D) ? e[lane + 64 * j] : make_float4(0.f, 0.f, 0.f, 0.f);
-    }
-#pragma unroll
-    for (int r = 0; r < FIN_ROWS; r++) {
-        const int m = w + 16 * r;
-        if (m >= g.M) continue;
-        const int tok = tokr[r];
-        if (g.prefill) {
-            if (lane == 0) g.ids[m] = tok;
-            continue;
-        }
-        const bool greedy = t >= nf[r] - 1;
-        if (lane == 0) {
+        for (int c = 4 * tid; c < g.D; c += 4 * FIN_THR)
+            *reinterpret_cast<float4 *>(g.x_next + (g.pk ? pk_index(m, c, g.ldx) : (size_t)m * g.ldx + c)) = e[c / 4];
+        if (tid == 0) {
             g.ids[(size_t)t * g.M + m] = tok;
-            g.pos[m] = ps[r] + 1;
+            g.pos[m] = ps + 1;
             // rows that stopped in an earlier step stay stopped
-            const int dr = rd[r] | (g.eos >= 0 && greedy && tok == g.eos);
+            const int dr = rd | (g.eos >= 0 && t >= nf - 1 && tok == g.eos);
             g.row_done[m] = dr;
-            if (!dr) atomicAnd(&s_all, 0);
-        }
-        // the next step's embedding row (embedding.c:79-84)
-#pragma unroll
-        for (int j = 0; j < CPL; j++) {
-            const int c = 4 * (lane + 64 * j);
-            if (c < g.D)
-                *reinterpret_cast<float4 *>(g.x_next + (g.pk ? pk_index(m, c, g.ldx) : (size_t)m * g.ldx + c)) = ev[r][j];
+            put(rf, m, __builtin_bit_cast(float, dr), tag);
         }
     }
     BTRACE(g.st, g.kslot + 1, 4);
-    __syncthreads();
+    if (!arrive_last(g.head_cnt, gridDim.x, &s_flag)) return;
     BTRACE(g.st, g.kslot + 1, 1);
-    if (tid == 0) {
-        if (!g.prefill) {
-            g.st->t = t + 1;
-            *g.steps_done = t + 1;
-            if (s_all) g.st->done = 1;
+    if (w == 0) {
+        int all = g.eos >= 0;
+        if (dec && all)
+            for (int b = lane; b < g.M; b += 64) {
+                u2 p = __builtin_bit_cast(u2, __builtin_amdgcn_raw_buffer_load_b64(rf, (unsigned)(b * 8), 0, CP_SC1));
+                for (unsigned spin = 0; p.y != tag && spin < SPIN_CAP; spin++) {
+                    __builtin_amdgcn_s_sleep(1);
+                    p = __builtin_bit_cast(u2, __builtin_amdgcn_raw_buffer_load_b64(rf, (unsigned)(b * 8), 0, CP_SC1));
+                }
+                all &= p.x != 0u;
+            }
+        all = __all(all);
+        if (tid == 0) {
+            if (dec) {
+                g.st->t = t + 1;
+                *g.steps_done = t + 1;
+                if (all) g.st->done = 1;
+            }
+            g.st->tag = g.st->tag + 1;
         }
-        g.st->tag = g.st->tag + 1;
     }
 }
 
@@ -1109,8 +1080,8 @@ hipError_t launch_gemm(int epi, bool norm, bool bf16, bool prefill, const GemmAr
 }
 
 hipError_t launch_head_finish(const GemmArgs &g, hipStream_t stream) {
-    if (g.M > BK_MAXM) return hipErrorInvalidValue;
-    hipLaunchKernelGGL(head_finish_kernel, dim3(1), dim3(FIN_THR), 0, stream, g);
+    if (g.M < 1 || g.M > BK_MAXM || !g.fin || !g.head_cnt) return hipErrorInvalidValue;
+    hipLaunchKernelGGL(head_finish_kernel, dim3(g.M), dim3(FIN_THR), 0, stream, g);
     return hipGetLastError();
 }
 
