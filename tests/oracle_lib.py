@@ -109,6 +109,13 @@ class Model:
             out.append(np.ctypeslib.as_array(p, shape=(n.value,)).copy())
         return out
 
+    def param_view(self, i):
+        """Parameter i of the oracle model (0: embedding, then 12 per layer,
+        then the final gamma and the lm_head bias) as a writable view."""
+        n = C.c_longlong()
+        p = lib().orc_model_param(self.ptr, i, C.byref(n))
+        return np.ctypeslib.as_array(p, shape=(n.value,))
+
     def round_weights_bf16(self):
         """Rounds every weight matrix (embedding, qkv, out, gate, up, down) to
         bf16 in place (round to nearest even, stored back as fp32): the W16A32
