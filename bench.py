@@ -232,6 +232,7 @@ def decode_run(L, cfg, steps, warmup, grid=0, bf16=False):
         s.set_grid(grid)
     feed = prompts(L, cfg, V, P, B)
     ids, _ = s.decode(feed, P)                      # prompt, one token per step
+    first_ids = ids[-1].copy()
     if warmup:
         ids, _ = s.decode(ids[-1:], warmup)         # warmup (greedy)
     start_pos = int(s.lengths()[0])
@@ -244,7 +245,16 @@ def decode_run(L, cfg, steps, warmup, grid=0, bf16=False):
     nbytes = step_bytes(V, D, Ly, F, positions, B, bf16)
     achieved = nbytes / (dev_ms * 1e-3) / 1e9
     kern = s.kernel()
+    # time to the first generated token: the prompt again on the reset
+    # session, one token per step as decoder_lm_generate feeds it
+    # (gpt.c:306-344); its last step emits the first greedy token
+    s.reset()
+    t0 = time.perf_counter()
+    again, _ = s.decode(feed, P)
+    ttft = time.perf_counter() - t0
+    assert (again[-1] == first_ids).all()
     return {
+        "first_token": {"prompt_tokens": P, "ms": round(ttft * 1e3, 3), "device_ms": round(s.last_ms(), 3)},
         "tok_s": B * steps / wall, "ms_per_step": wall * 1e3 / steps, "device_ms_per_step": dev_ms / steps,
         "achieved": achieved, "nbytes": nbytes, "kernel": kern, "grid": s.grid(), "B": B,
         "positions": [start_pos, start_pos + steps - 1], "P": P,
@@ -424,8 +434,9 @@ def summary(r):
     out = {"tokens_per_s": round(r["tok_s"], 2), "ms_per_step": round(r["ms_per_step"], 5),
            "batch": r["B"], "roofline_achieved_GBps": round(r["achieved"], 1),
            "roofline_frac": round(r["achieved"] / 8000.0, 4), "kernel": r["kernel_desc"]}
-    if "prefill" in r:
-        out["prefill"] = r["prefill"]
+    for k in ("prefill", "first_token"):
+        if k in r:
+            out[k] = r[k]
     return out
 
 
@@ -486,8 +497,9 @@ def main():
                      "frac": round(r["achieved"] / 8000.0, 4), "traffic": None,
                      "kernel": r["kernel_desc"], "algorithmic_bytes_per_launch": r["nbytes"]},
     }
-    if "prefill" in r:
-        line["prefill"] = r["prefill"]
+    for k in ("prefill", "first_token"):
+        if k in r:
+            line[k] = r[k]
     positions = range(r["positions"][0], r["positions"][1] + 1)
     traffic, prof = measured_traffic(cfg, positions) if cfg not in ("c4", "c5") and not args.bf16 else (None, None)
     line["roofline"]["traffic"] = traffic
