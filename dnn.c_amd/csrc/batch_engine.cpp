@@ -37,12 +37,25 @@ constexpr int CNT_TOTAL = CNT_GEMM + CNT_ATT + 1;
 
 inline int round_up(int v, int a) { return (v + a - 1) / a * a; }
 
+// Workgroups a decode GEMM without rms_norm is split towards (read once, so
+// the partial buffers sized at engine creation match every launch);
+// DNN_HIP_KS_FILL overrides.  Measured at 32 rows (C3): 64 -> 66.1k tokens/s,
+// 128 / 192 / 256 / 384 -> 64.4k / 64.3k / 63.8k / 63.2k (out_proj split over
+// 2..4 workgroups per tile); 8 rows: 192 0.6% slower; 64 rows within noise.
+int ks_fill() {
+    static const int v = [] {
+        const char *e = getenv("DNN_HIP_KS_FILL");
+        return e ? std::max(1, atoi(e)) : 64;
+    }();
+    return v;
+}
+
 // Split of a decode GEMM: k-steps per wavefront (kpw, one of GEMM_KPW) and
 // workgroups per column tile (ks), K/16 = 4 * ks * kpw.  A wavefront holds all
 // of its A and W loads in registers at once, which bounds kpw by the row tiles
 // per workgroup (mt_max, 0 = all); a GEMM without rms_norm is split further
-// until it has 64 workgroups (the split's partials and last-arriver cost more
-// than the extra parallelism gains below that).
+// until it has ks_fill() workgroups (the split's partials and last-arriver cost
+// more than the extra parallelism gains below that).
 int pick_ks(int ntiles, int K, int M, bool norm, int mt_max = 0) {
     const int nks = K / 16, tiles_m = (M + 15) / 16;
     const int mt = mt_max > 0 && tiles_m > mt_max ? mt_max : tiles_m;
@@ -55,7 +68,7 @@ int pick_ks(int ntiles, int K, int M, bool norm, int mt_max = 0) {
         const int ks = nks / (4 * kpw);
         if (ks > 8) break;
         best = ks;
-        if (norm || ntiles * ks * row_groups >= 64) break;
+        if (norm || ntiles * ks * row_groups >= ks_fill()) break;
     }
     return best;
 }
