@@ -42,16 +42,15 @@ struct StepState {
 
 // C[m][n] = sum_k A[m][k] * W[n][k] (+ epilogue).  A: fp32 rows of lda floats
 // (logical row m is physical row arow[m] when arow is set); W: out-major rows of
-// ldw elements (fp32 or bf16), zero-padded past the true K.  K (a multiple of 16)
-// counts the padded columns; A's padding columns are zero.
+// ldw elements (fp32 or bf16), zero-padded past the true K, read from its
+// fragment-ordered copy Wp.  K (a multiple of 16) counts the padded columns;
+// A's padding columns are zero.
 struct GemmArgs {
     const float *A;
     const int *arow;
     int lda, M, mpad;           // mpad: rows the A buffer holds (loads past it read 0)
-    const void *W;              // fp32 or bf16 elements
-    size_t w_bytes;             // bytes from W to the end of its arena (loads past it read 0)
-    const void *Wp;             // the same matrix in fragment order (decode shape), or null
-    size_t wp_bytes;            // bytes of the packed matrix
+    const void *Wp;             // W in fragment order (fp32 or bf16 elements; see pack_kernel)
+    size_t wp_bytes;            // bytes of the packed matrix (loads past it read 0)
     int pk;                     // 1 (decode steps): A, the residual, the RES / SWIGLU outputs and the
                                 // next step's embedding rows are in fragment order (pk_index)
     int ldw, N, K;

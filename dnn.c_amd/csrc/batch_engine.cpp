@@ -285,19 +285,10 @@ int engine_get(dnn_hip_session *s, int rows, int layout = 0) {
 struct Wts {
     const dnn_hip_model *m;
     const float *f(uint32_t off) const { return reinterpret_cast<const float *>(m->arena) + off; }
-    const void *w(uint32_t off) const {
-        return m->bf16 ? static_cast<const void *>(m->arena16 + off) : static_cast<const void *>(f(off));
-    }
-    size_t w_bytes(uint32_t off) const {
-        const size_t es = m->bf16 ? 2 : 4;
-        return (m->arena_bytes / 4 - off) * es;
-    }
 };
 
-GemmArgs gemm_base(dnn_hip_session *s, const Wts &W, uint32_t woff, size_t pk, int ldw, int N, int K) {
+GemmArgs gemm_base(dnn_hip_session *s, size_t pk, int ldw, int N, int K) {
     GemmArgs g{};
-    g.W = W.w(woff);
-    g.w_bytes = W.w_bytes(woff);
     const size_t es = s->m->bf16 ? 2 : 4;
     g.Wp = static_cast<const char *>(s->m->packed) + pk * es;
     g.wp_bytes = (size_t)((N + 15) / 16) * 16 * (size_t)ldw * es;
@@ -333,7 +324,7 @@ int enqueue_layer(dnn_hip_session *s, int l, const PrefillPlan *pp) {
     const bool bf = m->bf16 != 0;
     const MtPlan mp = mt_plan(M, true);
 
-    GemmArgs g = gemm_base(s, W, lo.wqkv, m->pk_l[(size_t)l * 4 + 0], ldD, 3 * D, ldD);
+    GemmArgs g = gemm_base(s, m->pk_l[(size_t)l * 4 + 0], ldD, 3 * D, ldD);
     g.A = e->X; g.lda = ldD; g.M = M;
     if (!pre) g.mt_max = mp.qkv;
     g.ks = pre ? 1 : pick_ks((3 * D + 15) / 16, ldD, M, true, g.mt_max);
@@ -367,7 +358,7 @@ int enqueue_layer(dnn_hip_session *s, int l, const PrefillPlan *pp) {
         HIP_TRY(launch_attn(a, s->stream));
     }
 
-    g = gemm_base(s, W, lo.wo, m->pk_l[(size_t)l * 4 + 1], ldD, D, ldD);
+    g = gemm_base(s, m->pk_l[(size_t)l * 4 + 1], ldD, D, ldD);
     g.A = e->ATT; g.lda = ldD; g.M = M;
     g.bias = W.f(lo.bo);
     g.out = e->X1; g.ldo = ldD; g.res = e->X; g.ldr = ldD;
@@ -377,7 +368,7 @@ int enqueue_layer(dnn_hip_session *s, int l, const PrefillPlan *pp) {
     g.pk = !pre;
     HIP_TRY(launch_gemm(EPI_RES, false, bf, pre, g, s->stream));
 
-    g = gemm_base(s, W, lo.wgu, m->pk_l[(size_t)l * 4 + 2], ldD, 2 * m->F, ldD);
+    g = gemm_base(s, m->pk_l[(size_t)l * 4 + 2], ldD, 2 * m->F, ldD);
     g.A = e->X1; g.lda = ldD; g.M = M;
     g.bias = W.f(lo.bg); g.bias2 = W.f(lo.bu);
     g.gamma = W.f(lo.g_ffn); g.eps = lo.eps_ffn; g.dnorm = D;
@@ -389,7 +380,7 @@ int enqueue_layer(dnn_hip_session *s, int l, const PrefillPlan *pp) {
     g.pk = !pre;
     HIP_TRY(launch_gemm(EPI_SWIGLU, true, bf, pre, g, s->stream));
 
-    g = gemm_base(s, W, lo.wd, m->pk_l[(size_t)l * 4 + 3], ldF, D, ldF);
+    g = gemm_base(s, m->pk_l[(size_t)l * 4 + 3], ldF, D, ldF);
     g.A = e->ACT; g.lda = ldF; g.M = M;
     g.bias = W.f(lo.bd);
     g.out = e->X; g.ldo = ldD; g.res = e->X1; g.ldr = ldD;
@@ -409,7 +400,7 @@ int enqueue_head(dnn_hip_session *s, const PrefillPlan *pp, float *logits, int *
     const Wts W{m};
     const uint32_t embed = (uint32_t)(m->off.embed / 4), lm_bias = (uint32_t)(m->off.lm_bias / 4),
                    g_final = (uint32_t)(m->off.g_final / 4);
-    GemmArgs g = gemm_base(s, W, embed, m->pk_embed, m->ldD, m->V, m->ldD);
+    GemmArgs g = gemm_base(s, m->pk_embed, m->ldD, m->V, m->ldD);
     g.A = e->X; g.lda = m->ldD; g.M = rows > 0 ? rows : s->B;
     g.arow = pp ? pp->arow : nullptr;
     g.bias = W.f(lm_bias);

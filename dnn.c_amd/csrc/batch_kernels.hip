@@ -165,9 +165,8 @@ __global__ __launch_bounds__(64 * WM * WN * KW) void gemm_kernel(const GemmArgs 
     const int kb0 = part * nks / parts, kb1 = (part + 1) * nks / parts;
 
     const rsrc_t ra = buf(g.A, (size_t)g.mpad * g.lda * 4);
-    const rsrc_t rw = buf(g.W, g.w_bytes);
     const rsrc_t rg = buf(g.gamma, NORM ? (size_t)g.K * 4 : 0);
-    unsigned aoff[MT], woff[NT];
+    unsigned aoff[MT];
 #pragma unroll
     for (int mt = 0; mt < MT; mt++) {
         const int m = tile_m * BM + wm * 16 * MT + 16 * mt + r16;
@@ -180,11 +179,6 @@ __global__ __launch_bounds__(64 * WM * WN * KW) void gemm_kernel(const GemmArgs 
     }
     // bytes between consecutive 16-column k-blocks of A
     const unsigned astep = g.pk ? 1024u : 64u;
-#pragma unroll
-    for (int nt = 0; nt < NT; nt++) {
-        const int n = tile_n * BN + wn * 16 * NT + 16 * nt + r16;
-        woff[nt] = (unsigned)((size_t)n * g.ldw + 4 * q4);     // elements
-    }
 
     f4 acc[MT][NT];
 #pragma unroll
@@ -293,12 +287,23 @@ __global__ __launch_bounds__(64 * WM * WN * KW) void gemm_kernel(const GemmArgs 
         for (int u = 0; u < KPW; u++) kstep(a[u], b[u], gm[u]);
         BTRACE(g.st, g.kslot, 1);
     } else {
+        // weights from the fragment-ordered copy: one contiguous 1 KB (fp32)
+        // or 512 B (bf16) per wavefront load instead of 16 separate 64-byte
+        // pieces of row-major rows (C4 prefill 69 -> 78 TFLOP/s)
+        const rsrc_t rwp = buf(g.Wp, g.wp_bytes);
+        const int nkb = g.ldw / 16;
+        unsigned pb[NT];
+#pragma unroll
+        for (int nt = 0; nt < NT; nt++) {
+            const int t16 = tile_n * WN * NT + wn * NT + nt;
+            pb[nt] = (unsigned)(((size_t)t16 * nkb * 64 + lane) * 4);
+        }
         for (int kb = kb0; kb < kb1; kb += U) {
             f4 a[U][MT], b[U][NT], gm[U];
 #pragma unroll
             for (int u = 0; u < U; u++) {
 #pragma unroll
-                for (int nt = 0; nt < NT; nt++) b[u][nt] = ldw4<BF>(rw, woff[nt] + (unsigned)((kb + u) * 16));
+                for (int nt = 0; nt < NT; nt++) b[u][nt] = ldw4<BF>(rwp, pb[nt] + (unsigned)((kb + u) * 256));
 #pragma unroll
                 for (int mt = 0; mt < MT; mt++) a[u][mt] = lda4(ra, aoff[mt] + (unsigned)((kb + u) * 64));
                 if (NORM) gm[u] = lda4(rg, (unsigned)(((kb + u) * 16 + 4 * q4) * 4));
