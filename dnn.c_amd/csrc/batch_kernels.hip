@@ -36,6 +36,7 @@
 // order), and prefill (128 x 128 tiles, a 64 x 64 block per wavefront).
 
 #include "batch.h"
+#include <cstdio>
 #include <cstdlib>
 #include "decode_device.h"
 
@@ -944,6 +945,32 @@ __global__ __launch_bounds__(NTHR) void rms_rows_kernel(const float *x, const fl
 namespace {
 
 // decode shape: all rows in one tile (MT = rows / 16), k-steps per wavefront
+// Column tiles of a prefill GEMM: 128 or 96 columns per workgroup.  The
+// MFMA-bound prefill GEMMs run a CU's workgroups one after another in effect
+// (a launch of 1.05 workgroups per CU costs almost as much as one of 2), so
+// the busiest CU's work is its workgroups (rounded up over the device's CUs)
+// times their width.  A 96-column tile loads ~17% more per MFMA, so it is taken
+// only where it cuts that work by more than 5%.  Measured: 8 x 1024 rows (C4)
+// QKV (2304 columns) and out_proj / down (768) at 96, gate/up (4096) at 128:
+// prefill 78 -> 86 TFLOP/s; 1,332 rows (C3) 5.81 -> 5.08 ms; 12,718 rows (C5)
+// all at 128 (gate/up, 2048 columns, at 96 was 1-3% slower); 64-column tiles
+// were never faster.
+int prefill_nt(int N, int M) {
+    static const int cus = [] {
+        int dev = 0, n = 0;
+        if (hipGetDevice(&dev) != hipSuccess ||
+            hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n < 1)
+            n = 256;
+        return n;
+    }();
+    const int rows = (M + BK_PBM - 1) / BK_PBM;
+    auto cost = [&](int nt) {
+        const long long wgs = (long long)((N + 32 * nt - 1) / (32 * nt)) * rows;
+        return (wgs + cus - 1) / cus * nt;
+    };
+    return 20 * cost(3) < 19 * cost(4) ? 3 : 4;
+}
+
 // KPW = K / 16 / (4 * ks), chosen by the host among the instantiated values
 template <int EPI, bool NORM, bool BF, int MT>
 hipError_t gemm_decode_mt(const GemmArgs &g, hipStream_t st, int kw, int kpw) {
@@ -1009,8 +1036,23 @@ hipError_t gemm_decode(const GemmArgs &g, hipStream_t st) {
 
 template <int EPI, bool NORM, bool BF>
 hipError_t gemm_prefill(const GemmArgs &g, hipStream_t st) {
-    dim3 grid((g.N + BK_PBN - 1) / BK_PBN * g.ks, (g.M + BK_PBM - 1) / BK_PBM);
-    hipLaunchKernelGGL((gemm_kernel<4, 4, 2, 2, 1, 0, BF, EPI, NORM>), grid, dim3(NTHR), 0, st, g);
+    // 16-column tiles per wavefront (the workgroup covers 32 * NT columns):
+    // DNN_HIP_PREFILL_NT=q,r,s fixes them for the QKV, residual and SwiGLU
+    // GEMMs (0: chosen here)
+    static const int *req = [] {
+        static int v[3] = {0, 0, 0};
+        if (const char *e = getenv("DNN_HIP_PREFILL_NT")) sscanf(e, "%d,%d,%d", &v[0], &v[1], &v[2]);
+        return v;
+    }();
+    const int nt = req[EPI] >= 2 && req[EPI] <= 4 ? req[EPI] : prefill_nt(g.N, g.M);
+    const int bn = 32 * nt;
+    dim3 grid((g.N + bn - 1) / bn * g.ks, (g.M + BK_PBM - 1) / BK_PBM);
+    if (nt == 2)
+        hipLaunchKernelGGL((gemm_kernel<4, 2, 2, 2, 1, 0, BF, EPI, NORM>), grid, dim3(NTHR), 0, st, g);
+    else if (nt == 3)
+        hipLaunchKernelGGL((gemm_kernel<4, 3, 2, 2, 1, 0, BF, EPI, NORM>), grid, dim3(NTHR), 0, st, g);
+    else
+        hipLaunchKernelGGL((gemm_kernel<4, 4, 2, 2, 1, 0, BF, EPI, NORM>), grid, dim3(NTHR), 0, st, g);
     return hipGetLastError();
 }
 
