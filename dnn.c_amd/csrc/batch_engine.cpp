@@ -15,6 +15,7 @@
 // vision_lm_generate's prefix prefill (vlm.c:497-517) need it -- and returns the
 // greedy token of each sequence's last new row.
 #include <algorithm>
+#include <array>
 #include <cstring>
 #include <vector>
 
@@ -280,6 +281,24 @@ int engine_get(dnn_hip_session *s, int rows, int layout = 0) {
         e->layout = 0;
     }
     return set_layout(s, layout);
+}
+
+// Attention tiles (batch row, first new row) of a prefill, heaviest first: by
+// the keys the tile's last row sees, as prefill_attn_kernel counts them, ties
+// in building order.  The kernel's workgroups are dispatched tile-major, so
+// the longest start first and the launch ends on the shortest.
+std::vector<int> prefill_tiles(int B, const int *nn, const int *p0, int mode, int prefix_len) {
+    std::vector<std::array<int, 3>> t;
+    for (int b = 0; b < B; b++)
+        for (int t0 = 0; t0 < nn[b]; t0 += 64) {
+            int kv_end = p0[b] + t0 + std::min(64, nn[b] - t0);
+            if (mode == 1 && kv_end < prefix_len) kv_end = prefix_len;
+            t.push_back({std::min(kv_end, p0[b] + nn[b]), b, t0});
+        }
+    std::stable_sort(t.begin(), t.end(), [](const std::array<int, 3> &x, const std::array<int, 3> &y) { return x[0] > y[0]; });
+    std::vector<int> out;
+    for (const auto &x : t) { out.push_back(x[1]); out.push_back(x[2]); }
+    return out;
 }
 
 struct Wts {
@@ -578,9 +597,7 @@ int engine_prefill(dnn_hip_session *s, const float *embeds, int n_embed, const i
     if (rc) return rc;
     BatchEngine *e = s->eng;
     // the plan: row_b, row_p, pid [M]; row0, n_new, p0, arow [B]; tiles [T][2]
-    std::vector<int> tiles;
-    for (int b = 0; b < B; b++)
-        for (int t0 = 0; t0 < nn[b]; t0 += 64) { tiles.push_back(b); tiles.push_back(t0); }
+    const std::vector<int> tiles = prefill_tiles(B, nn.data(), p0.data(), mode, prefix_len);
     const int T = (int)tiles.size() / 2;
     std::vector<int> plan((size_t)3 * M + 4 * B + tiles.size());
     int *row_b = plan.data(), *row_p = row_b + M, *pid = row_p + M, *hrow0 = pid + M, *hnn = hrow0 + B,
@@ -652,9 +669,8 @@ int engine_block(dnn_hip_session *s, int layer, const float *x, int n_new, int p
     int rc = engine_get(s, M);
     if (rc) return rc;
     BatchEngine *e = s->eng;
-    std::vector<int> tiles;
-    for (int b = 0; b < B; b++)
-        for (int t0 = 0; t0 < n_new; t0 += 64) { tiles.push_back(b); tiles.push_back(t0); }
+    const std::vector<int> bn(B, n_new), bp(B, pos0);
+    const std::vector<int> tiles = prefill_tiles(B, bn.data(), bp.data(), mode, prefix_len);
     const int T = (int)tiles.size() / 2;
     std::vector<int> plan((size_t)3 * M + 4 * B + tiles.size());
     int *row_b = plan.data(), *row_p = row_b + M, *pid = row_p + M, *hrow0 = pid + M, *hnn = hrow0 + B,

@@ -781,13 +781,13 @@ __global__ __launch_bounds__(64 * AW) void attn_kernel(const AttnArgs a) {
 // ---------------------------------------------------------------------------
 // Prefill attention (the multi-token cached forward, transformer.c:256-397,
 // and the full-sequence triangular form, attention.c:259-380).  Workgroup
-// (64-row tile of one sequence's new rows, head h); wavefront w owns rows
-// 16w .. 16w+15 of the tile.  Per 64-key tile: K^T and V staged in LDS,
-// S = Q K^T on MFMA (A: Q rows from registers, B: K^T from LDS), the causal /
-// prefix-LM mask (transformer.c:305-325: a row at position p sees keys
-// j < (p < prefix_len ? prefix_len : p + 1) in prefix-LM mode, j <= p
-// otherwise), running max / sum per row, P through LDS into the A layout, and
-// O += P V on MFMA.
+// (64-row tile of one sequence's new rows, head h), tiles heaviest first;
+// wavefront w owns rows 16w .. 16w+15 of the tile.  Per 64-key tile: K^T and
+// V staged in LDS, S = Q K^T on MFMA (A: Q rows from registers, B: K^T from
+// LDS), the causal / prefix-LM mask (transformer.c:305-325: a row at
+// position p sees keys j < (p < prefix_len ? prefix_len : p + 1) in prefix-LM
+// mode, j <= p otherwise), running max / sum per row, P through LDS into the
+// A layout, and O += P V on MFMA.
 __global__ __launch_bounds__(NTHR) void prefill_attn_kernel(const PrefillAttnArgs a) {
     __shared__ float Ks[BK_DK][65];
     __shared__ float Vs[64][BK_DK + 1];
@@ -795,7 +795,8 @@ __global__ __launch_bounds__(NTHR) void prefill_attn_kernel(const PrefillAttnArg
     const int tid = threadIdx.x, lane = tid & 63;
     const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int r16 = lane & 15, q4 = lane >> 4;
-    const int tile = blockIdx.x, h = blockIdx.y;
+    // tile-major: every head of the heaviest tile first (the host orders the tiles)
+    const int tile = blockIdx.x / a.H, h = blockIdx.x - tile * a.H;
     const int b = a.tiles[2 * tile], t0 = a.tiles[2 * tile + 1];
     const int nn = a.n_new[b], p0 = a.p0[b], r0 = a.row0[b];
     const int nq = min(64, nn - t0);
@@ -1144,7 +1145,7 @@ hipError_t launch_attn(const AttnArgs &a, hipStream_t stream) {
 }
 
 hipError_t launch_prefill_attn(const PrefillAttnArgs &a, hipStream_t stream) {
-    hipLaunchKernelGGL(prefill_attn_kernel, dim3(a.n_tiles, a.H), dim3(NTHR), 0, stream, a);
+    hipLaunchKernelGGL(prefill_attn_kernel, dim3(a.n_tiles * a.H), dim3(NTHR), 0, stream, a);
     return hipGetLastError();
 }
 
