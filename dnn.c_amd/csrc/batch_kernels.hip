@@ -138,7 +138,9 @@ __global__ __launch_bounds__(64 * WM * WN * KW) void gemm_kernel(const GemmArgs 
     constexpr int GT = 64 * WM * WN * KW;                  // threads
     constexpr int BM = 16 * MT * WM, BN = 16 * NT * WN;
     constexpr int LDR = BN + 1;
-    constexpr int U = 4;                                   // k-steps per loop iteration (prefill shape)
+    // k-steps per loop iteration (prefill shape; on C4 two beat four by 2.6%
+    // and one by 13%)
+    constexpr int U = 2;
     __shared__ float red[KW][BM][LDR];
     __shared__ float ssl[KW][BM];
     __shared__ int s_flag;
