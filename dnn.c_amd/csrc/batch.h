@@ -51,8 +51,8 @@ struct GemmArgs {
     int lda, M, mpad;           // mpad: rows the A buffer holds (loads past it read 0)
     const void *Wp;             // W in fragment order (fp32 or bf16 elements; see pack_kernel)
     size_t wp_bytes;            // bytes of the packed matrix (loads past it read 0)
-    int pk;                     // 1 (decode steps): A, the residual, the RES / SWIGLU outputs and the
-                                // next step's embedding rows are in fragment order (pk_index)
+    int pk;                     // 1 (decode steps and prefill): A, the residual, the RES / SWIGLU outputs
+                                // and the next step's embedding rows are in fragment order (pk_index)
     int ldw, N, K;
     int ks;                     // workgroups per column tile (split K), >= 1
     int mt_max;                 // decode shape: at most this many 16-row tiles per workgroup (0: all rows)
@@ -128,14 +128,17 @@ struct PrefillAttnArgs {
     int ldatt;
     int mode, prefix_len;
     StepState *st;
+    int pk;                     // att rows in fragment order (pk_index)
 };
 
 // Embedding rows: out[m] = embed[ids[m]] (ids: feed row 0 of a decode call, or
-// prefill token ids); rows with ids < 0 are left alone.
+// prefill token ids); rows with ids < 0 take row m of src when it is set (an
+// embedding input staged row-major), else are left alone.
 struct EmbedArgs {
     const float *embed;
     const int *ids;
     float *out;
+    const float *src;           // rows with ids < 0: copied from these row-major rows of ld floats (or left alone)
     int M, ld, D;
     int pk;                     // out in fragment order (pk_index)
     StepState *st;              // non-null: reset the step counters of a decode call

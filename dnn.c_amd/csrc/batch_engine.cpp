@@ -330,6 +330,7 @@ struct PrefillPlan {
     int M;
     const int *row_b, *row_p, *pid, *row0, *n_new, *p0, *arow, *tiles;
     int n_tiles, mode, prefix_len;
+    int pk;             // activations in fragment order (engine_prefill), else row-major
 };
 
 int enqueue_layer(dnn_hip_session *s, int l, const PrefillPlan *pp) {
@@ -339,6 +340,7 @@ int enqueue_layer(dnn_hip_session *s, int l, const PrefillPlan *pp) {
     const LayerOff &lo = m->h_layers[l];
     const int D = m->D, ldD = m->ldD, ldF = m->ldF;
     const bool pre = pp != nullptr;
+    const int pk = !pre || pp->pk;          // activations in fragment order
     const int M = pre ? pp->M : s->B;
     const bool bf = m->bf16 != 0;
     const MtPlan mp = mt_plan(M, true);
@@ -356,7 +358,7 @@ int enqueue_layer(dnn_hip_session *s, int l, const PrefillPlan *pp) {
     g.H = m->H; g.kv_s = s->kv_s; g.B = s->B; g.layer = l;
     g.rope = m->rope; g.rope_rows = m->rope_rows;
     g.kslot = 5 * l;
-    g.pk = !pre;
+    g.pk = pk;
     HIP_TRY(launch_gemm(EPI_QKV, true, bf, pre, g, s->stream));
 
     if (pre) {
@@ -364,7 +366,7 @@ int enqueue_layer(dnn_hip_session *s, int l, const PrefillPlan *pp) {
         a.q = e->Q; a.att = e->ATT; a.kc = s->kc; a.vc = s->vc;
         a.row0 = pp->row0; a.n_new = pp->n_new; a.p0 = pp->p0; a.tiles = pp->tiles;
         a.n_tiles = pp->n_tiles; a.H = m->H; a.kv_s = s->kv_s; a.layer = l; a.D = D; a.B = s->B; a.ldatt = ldD;
-        a.mode = pp->mode; a.prefix_len = pp->prefix_len; a.st = e->st;
+        a.mode = pp->mode; a.prefix_len = pp->prefix_len; a.st = e->st; a.pk = pk;
         HIP_TRY(launch_prefill_attn(a, s->stream));
     } else {
         AttnArgs a{};
@@ -384,7 +386,7 @@ int enqueue_layer(dnn_hip_session *s, int l, const PrefillPlan *pp) {
     if (!pre) g.mt_max = mp.out;
     g.ks = pre ? 1 : pick_ks((D + 15) / 16, ldD, M, false, g.mt_max);
     g.part = e->part; g.cnt = e->cnt; g.kslot = 5 * l + 2;
-    g.pk = !pre;
+    g.pk = pk;
     HIP_TRY(launch_gemm(EPI_RES, false, bf, pre, g, s->stream));
 
     g = gemm_base(s, m->pk_l[(size_t)l * 4 + 2], ldD, 2 * m->F, ldD);
@@ -396,7 +398,7 @@ int enqueue_layer(dnn_hip_session *s, int l, const PrefillPlan *pp) {
     g.ks = pre ? 1 : pick_ks((2 * m->F + 15) / 16, ldD, M, true, g.mt_max);
     g.part = e->part; g.cnt = e->cnt;
     g.kslot = 5 * l + 3;
-    g.pk = !pre;
+    g.pk = pk;
     HIP_TRY(launch_gemm(EPI_SWIGLU, true, bf, pre, g, s->stream));
 
     g = gemm_base(s, m->pk_l[(size_t)l * 4 + 3], ldF, D, ldF);
@@ -406,7 +408,7 @@ int enqueue_layer(dnn_hip_session *s, int l, const PrefillPlan *pp) {
     if (!pre) g.mt_max = mp.down;
     g.ks = pre ? 1 : pick_ks((D + 15) / 16, ldF, M, false, g.mt_max);
     g.part = e->part; g.cnt = e->cnt; g.kslot = 5 * l + 4;
-    g.pk = !pre;
+    g.pk = pk;
     HIP_TRY(launch_gemm(EPI_RES, false, bf, pre, g, s->stream));
     return DNN_HIP_OK;
 }
@@ -431,7 +433,7 @@ int enqueue_head(dnn_hip_session *s, const PrefillPlan *pp, float *logits, int *
     g.x_next = e->X; g.ldx = m->ldD; g.embed = W.f(embed);
     g.steps_done = e->steps_done; g.eos = eos; g.row_done = e->row_done;
     g.prefill = pp != nullptr;
-    g.pk = pp == nullptr;                    // decode steps: X in fragment order
+    g.pk = pp == nullptr || pp->pk;          // decode steps and prefill: X in fragment order
     g.kslot = 5 * m->L;
     g.mt_max = mt_plan(g.M, pp == nullptr).head;
     g.ks = pick_ks((m->V + 15) / 16, m->ldD, g.M, true, g.mt_max);
@@ -593,7 +595,7 @@ int engine_prefill(dnn_hip_session *s, const float *embeds, int n_embed, const i
         M += nn[b];
     }
     HIP_TRY(hipSetDevice(m->device));
-    int rc = engine_get(s, M);
+    int rc = engine_get(s, M, 1);            // activations in fragment order, as decode keeps them
     if (rc) return rc;
     BatchEngine *e = s->eng;
     // the plan: row_b, row_p, pid [M]; row0, n_new, p0, arow [B]; tiles [T][2]
@@ -622,16 +624,20 @@ int engine_prefill(dnn_hip_session *s, const float *embeds, int n_embed, const i
     if (rc) return rc;
     int *d = e->pre_i;
     PrefillPlan pp{M, d, d + M, d + 2 * M, d + 3 * M, d + 3 * M + B, d + 3 * M + 2 * B, d + 3 * M + 3 * B,
-                   d + 3 * M + 4 * B, T, mode, prefix_len};
-    // embedding inputs (e.g. image patches) straight into their rows, token rows gathered
+                   d + 3 * M + 4 * B, T, mode, prefix_len, 1};
+    // embedding inputs (e.g. image patches) staged row-major in the attention
+    // buffer (free until the first layer's attention), then every row into X
+    // in fragment order: those copied, token rows gathered
     if (n_embed > 0)
         for (int b = 0; b < B && !rc; b++)
-            rc = stage_copy2d(s, e->X + (size_t)row0[b] * m->ldD, (size_t)m->ldD * 4, embeds + (size_t)b * n_embed * D,
+            rc = stage_copy2d(s, e->ATT + (size_t)row0[b] * m->ldD, (size_t)m->ldD * 4, embeds + (size_t)b * n_embed * D,
                               (size_t)D * 4, (size_t)D * 4, n_embed);
     if (rc) return rc;
     EmbedArgs ea{};
     ea.embed = reinterpret_cast<const float *>(m->arena) + m->off.embed / 4;
     ea.ids = pp.pid; ea.out = e->X; ea.M = M; ea.ld = m->ldD; ea.D = D;
+    ea.src = n_embed > 0 ? e->ATT : nullptr;
+    ea.pk = 1;
     HIP_TRY(launch_embed(ea, s->stream));
     HIP_TRY(hipEventRecord(s->ev0, s->stream));
     for (int l = 0; l < m->L; l++) {

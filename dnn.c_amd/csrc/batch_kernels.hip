@@ -177,8 +177,9 @@ __global__ __launch_bounds__(64 * WM * WN * KW) void gemm_kernel(const GemmArgs 
         // a row map only where one is used (a possible load here would make
         // every later wait cover it)
         if (AROW) pm = g.arow[m < g.M ? m : 0];
-        aoff[mt] = g.pk ? (unsigned)((((size_t)(tile_m * (BM / 16) + wm * MT + mt) * (g.lda / 16)) * 64 + lane) * 16)
-                        : (unsigned)(((size_t)pm * g.lda + 4 * q4) * 4);
+        aoff[mt] = !g.pk ? (unsigned)(((size_t)pm * g.lda + 4 * q4) * 4)
+                   : AROW ? (unsigned)(pk_index(pm, 4 * q4, g.lda) * 4)      // one row's fragment pieces
+                          : (unsigned)((((size_t)(tile_m * (BM / 16) + wm * MT + mt) * (g.lda / 16)) * 64 + lane) * 16);
     }
     // bytes between consecutive 16-column k-blocks of A
     const unsigned astep = g.pk ? 1024u : 64u;
@@ -308,7 +309,7 @@ __global__ __launch_bounds__(64 * WM * WN * KW) void gemm_kernel(const GemmArgs 
 #pragma unroll
                 for (int nt = 0; nt < NT; nt++) b[u][nt] = ldw4<BF>(rwp, pb[nt] + (unsigned)((kb + u) * 256));
 #pragma unroll
-                for (int mt = 0; mt < MT; mt++) a[u][mt] = lda4(ra, aoff[mt] + (unsigned)((kb + u) * 64));
+                for (int mt = 0; mt < MT; mt++) a[u][mt] = lda4(ra, aoff[mt] + (unsigned)(kb + u) * astep);
                 if (NORM) gm[u] = lda4(rg, (unsigned)(((kb + u) * 16 + 4 * q4) * 4));
             }
 #pragma unroll
@@ -901,11 +902,12 @@ __global__ __launch_bounds__(NTHR) void prefill_attn_kernel(const PrefillAttnArg
     for (int v = 0; v < 4; v++) {
         const int i = 16 * w + 4 * q4 + v;
         if (i >= nq) continue;
-        float *o = a.att + (size_t)(r0 + t0 + i) * a.ldatt + h * BK_DK;
+        const int row = r0 + t0 + i;
         const float inv = lr[v];
 #pragma unroll
         for (int nt = 0; nt < 4; nt++) {
-            o[16 * nt + r16] = O[nt][v] / inv;
+            const int c = h * BK_DK + 16 * nt + r16;
+            a.att[a.pk ? pk_index(row, c, a.ldatt) : (size_t)row * a.ldatt + c] = O[nt][v] / inv;
         }
     }
 }
@@ -918,8 +920,8 @@ __global__ __launch_bounds__(NTHR) void embed_kernel(const EmbedArgs a) {
     if (m == 0 && threadIdx.x == 0 && a.st) { a.st->t = 0; a.st->done = 0; }
     if (threadIdx.x == 0 && a.row_done) a.row_done[m] = 0;
     const int id = a.ids[m];
-    if (id < 0) return;
-    const float *e = a.embed + (size_t)id * a.ld;
+    if (id < 0 && !a.src) return;
+    const float *e = id < 0 ? a.src + (size_t)m * a.ld : a.embed + (size_t)id * a.ld;
     for (int c = threadIdx.x; c < a.D; c += NTHR) a.out[a.pk ? pk_index(m, c, a.ld) : (size_t)m * a.ld + c] = e[c];
 }
 
