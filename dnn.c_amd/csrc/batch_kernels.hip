@@ -922,7 +922,11 @@ __global__ __launch_bounds__(NTHR) void embed_kernel(const EmbedArgs a) {
     const int id = a.ids[m];
     if (id < 0 && !a.src) return;
     const float *e = id < 0 ? a.src + (size_t)m * a.ld : a.embed + (size_t)id * a.ld;
-    for (int c = threadIdx.x; c < a.D; c += NTHR) a.out[a.pk ? pk_index(m, c, a.ld) : (size_t)m * a.ld + c] = e[c];
+    // four columns per thread: one 16-byte piece in either layout (D is a
+    // multiple of 64)
+    for (int c = 4 * threadIdx.x; c < a.D; c += 4 * NTHR)
+        *reinterpret_cast<float4 *>(a.out + (a.pk ? pk_index(m, c, a.ld) : (size_t)m * a.ld + c)) =
+            *reinterpret_cast<const float4 *>(e + c);
 }
 
 // ---------------------------------------------------------------------------
