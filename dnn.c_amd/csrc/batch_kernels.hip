@@ -954,16 +954,16 @@ __global__ __launch_bounds__(NTHR) void rms_rows_kernel(const float *x, const fl
 namespace {
 
 // decode shape: all rows in one tile (MT = rows / 16), k-steps per wavefront
-// Column tiles of a prefill GEMM: 128 or 96 columns per workgroup.  The
+// Column tiles of a prefill GEMM: 128, 96 or 64 columns per workgroup.  The
 // MFMA-bound prefill GEMMs run a CU's workgroups one after another in effect
 // (a launch of 1.05 workgroups per CU costs almost as much as one of 2), so
 // the busiest CU's work is its workgroups (rounded up over the device's CUs)
-// times their width.  A 96-column tile loads ~17% more per MFMA, so it is taken
-// only where it cuts that work by more than 5%.  Measured: 8 x 1024 rows (C4)
-// QKV (2304 columns) and out_proj / down (768) at 96, gate/up (4096) at 128:
-// prefill 78 -> 86 TFLOP/s; 1,332 rows (C3) 5.81 -> 5.08 ms; 12,718 rows (C5)
-// all at 128 (gate/up, 2048 columns, at 96 was 1-3% slower); 64-column tiles
-// were never faster.
+// times their width; the least work wins.  Ties go to 96 columns, then 64:
+// narrower tiles put more workgroups on a CU to hide each other's load
+// latency, and 96 loads a quarter less per MFMA than 64.  Measured against
+// 128 everywhere: 8 x 1024 rows (C4; QKV and out_proj / down at 96, gate/up
+// at 64) 78 -> 86 TFLOP/s when introduced; 12,718 rows, K = 512, bf16
+// weights (C5; all at 64) 70 -> 74; 1,332 rows (C3) 5.8 -> 4.4 ms.
 int prefill_nt(int N, int M) {
     static const int cus = [] {
         int dev = 0, n = 0;
@@ -977,7 +977,10 @@ int prefill_nt(int N, int M) {
         const long long wgs = (long long)((N + 32 * nt - 1) / (32 * nt)) * rows;
         return (wgs + cus - 1) / cus * nt;
     };
-    return 20 * cost(3) < 19 * cost(4) ? 3 : 4;
+    int best = 3;
+    if (cost(2) < cost(best)) best = 2;
+    if (cost(4) < cost(best)) best = 4;
+    return best;
 }
 
 // KPW = K / 16 / (4 * ks), chosen by the host among the instantiated values
