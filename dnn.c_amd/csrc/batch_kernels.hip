@@ -786,7 +786,7 @@ __global__ __launch_bounds__(64 * AW) void attn_kernel(const AttnArgs a) {
 // and the full-sequence triangular form, attention.c:259-380).  Workgroup
 // (64-row tile of one sequence's new rows, head h), tiles heaviest first;
 // wavefront w owns rows 16w .. 16w+15 of the tile.  Per 64-key tile: K^T and
-// V staged in LDS, S = Q K^T on MFMA (A: Q rows from registers, B: K^T from
+// V staged in LDS (loaded into registers one tile ahead), S = Q K^T on MFMA (A: Q rows from registers, B: K^T from
 // LDS), the causal / prefix-LM mask (transformer.c:305-325: a row at
 // position p sees keys j < (p < prefix_len ? prefix_len : p + 1) in prefix-LM
 // mode, j <= p otherwise), running max / sum per row, P through LDS into the
@@ -828,16 +828,27 @@ __global__ __launch_bounds__(NTHR) void prefill_attn_kernel(const PrefillAttnArg
 #pragma unroll
     for (int v = 0; v < 4; v++) { mr[v] = -INFINITY; lr[v] = 0.f; O[v] = f4{0.f, 0.f, 0.f, 0.f}; }
 
+    // this thread's share of a 64-key K^T / V tile, loaded one tile ahead:
+    // the next tile's loads are in flight while this one is computed
+    f4 kn[4], vn[4];
+    auto load_kv = [&](int key0) {
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const int rr = tid / 16 + 16 * i, cc = 4 * (tid % 16);
+            kn[i] = lda4(rk, (unsigned)(((size_t)rr * a.kv_s + key0 + cc) * 4));
+            vn[i] = lda4(rv, (unsigned)(((size_t)(key0 + rr) * BK_DK + cc) * 4));
+        }
+    };
+    if (kv_end > 0) load_kv(0);
     for (int key0 = 0; key0 < kv_end; key0 += 64) {
         __syncthreads();
 #pragma unroll
         for (int i = 0; i < 4; i++) {
             const int rr = tid / 16 + 16 * i, cc = 4 * (tid % 16);
-            const f4 kv = lda4(rk, (unsigned)(((size_t)rr * a.kv_s + key0 + cc) * 4));
-            Ks[rr][cc] = kv.x; Ks[rr][cc + 1] = kv.y; Ks[rr][cc + 2] = kv.z; Ks[rr][cc + 3] = kv.w;
-            const f4 vv = lda4(rv, (unsigned)(((size_t)(key0 + rr) * BK_DK + cc) * 4));
-            Vs[rr][cc] = vv.x; Vs[rr][cc + 1] = vv.y; Vs[rr][cc + 2] = vv.z; Vs[rr][cc + 3] = vv.w;
+            Ks[rr][cc] = kn[i].x; Ks[rr][cc + 1] = kn[i].y; Ks[rr][cc + 2] = kn[i].z; Ks[rr][cc + 3] = kn[i].w;
+            Vs[rr][cc] = vn[i].x; Vs[rr][cc + 1] = vn[i].y; Vs[rr][cc + 2] = vn[i].z; Vs[rr][cc + 3] = vn[i].w;
         }
+        if (key0 + 64 < kv_end) load_kv(key0 + 64);
         __syncthreads();
         f4 S[4];
 #pragma unroll
