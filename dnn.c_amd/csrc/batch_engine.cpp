@@ -219,6 +219,16 @@ int set_layout(dnn_hip_session *s, int layout) {
     return DNN_HIP_OK;
 }
 
+// Clear the step state's step count and stop flag before a prefill, block or
+// head launch: a decode call whose rows all stopped at eos leaves the flag set
+// (its later graph replays skip their work), and the GEMMs and the finisher
+// of these launches would skip theirs too.  A decode call clears both itself.
+int clear_step(dnn_hip_session *s) {
+    BatchEngine *e = s->eng;
+    HIP_TRY(hipMemsetAsync(&e->st->t, 0, sizeof(int) * 2, s->stream));   // t, done
+    return DNN_HIP_OK;
+}
+
 int engine_get(dnn_hip_session *s, int rows, int layout = 0) {
     dnn_hip_model *m = s->m;
     {
@@ -596,6 +606,7 @@ int engine_prefill(dnn_hip_session *s, const float *embeds, int n_embed, const i
     }
     HIP_TRY(hipSetDevice(m->device));
     int rc = engine_get(s, M, 1);            // activations in fragment order, as decode keeps them
+    if (!rc) rc = clear_step(s);
     if (rc) return rc;
     BatchEngine *e = s->eng;
     // the plan: row_b, row_p, pid [M]; row0, n_new, p0, arow [B]; tiles [T][2]
@@ -673,6 +684,7 @@ int engine_block(dnn_hip_session *s, int layer, const float *x, int n_new, int p
         return set_error(DNN_HIP_ERANGE, "position %d beyond the RoPE table (%d rows)", pos0 + n_new - 1, m->rope_rows);
     HIP_TRY(hipSetDevice(m->device));
     int rc = engine_get(s, M);
+    if (!rc) rc = clear_step(s);
     if (rc) return rc;
     BatchEngine *e = s->eng;
     const std::vector<int> bn(B, n_new), bp(B, pos0);
@@ -717,6 +729,7 @@ int engine_head(dnn_hip_session *s, const float *x, int n, int norm, float *logi
     if (!x || !logits || n < 1) return set_error(DNN_HIP_EINVAL, "bad head input (%d rows)", n);
     HIP_TRY(hipSetDevice(m->device));
     int rc = engine_get(s, n);
+    if (!rc) rc = clear_step(s);
     if (rc) return rc;
     BatchEngine *e = s->eng;
     std::vector<int> rows(n);

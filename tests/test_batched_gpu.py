@@ -230,3 +230,37 @@ def test_bf16_weights_match_rounded_oracle(B):
         want, wlg = m.generate(feed[:, b], 25, eos=-1, want_logits=True)
         assert list(ids[5:, b]) == list(want[6:]), "row %d" % b
         assert_logits_close(lg[5:, b], wlg, "row %d" % b)
+
+
+def test_prefill_block_head_after_every_row_stopped():
+    """An engine decode whose rows all stop at eos leaves the device step state
+    marked done (the rest of its graph replays skip their work).  A prefill,
+    a layer-level block and a head call on the same session afterwards must
+    still compute: each equals the same call on a fresh session."""
+    V, EOS = 512, 258
+    m = O.Model(V, 256, 2, 4, 683, 64, seed=23)
+    m.param_view(O.lib().orc_model_n_params(m.ptr) - 1)[EOS] = 50.0    # every step emits eos
+    hm = hip_model(m)
+    B = 8                                                               # the engine
+    r = np.random.default_rng(5)
+    feed = r.integers(0, V, size=(4, B)).astype(np.int32)
+    feed[feed == EOS] = 1
+    ids = r.integers(0, V, size=(B, 6)).astype(np.int32)
+    x = r.standard_normal((B, 3, 256)).astype(np.float32)
+    xh = r.standard_normal((5, 256)).astype(np.float32)
+
+    s = A.HipSession(hm, B, 64)
+    out, _ = s.decode(feed, 12, eos=EOS)
+    assert s.kernel() == 6 and len(out) < 12 and (out[-1] == EOS).all()
+    s.reset()
+    nxt, lg = s.prefill(ids=ids, want_logits=True)
+    y = s.block_forward(0, x, int(s.lengths()[0]))
+    h = s.head_forward(xh)
+
+    f = A.HipSession(hm, B, 64)
+    nxt_f, lg_f = f.prefill(ids=ids, want_logits=True)
+    y_f = f.block_forward(0, x, int(f.lengths()[0]))
+    h_f = f.head_forward(xh)
+    assert np.array_equal(nxt, nxt_f) and np.array_equal(lg, lg_f)
+    assert np.array_equal(y, y_f)
+    assert np.array_equal(h, h_f)
