@@ -20,6 +20,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include "engine_plan.h"
+
 namespace dnnhip {
 
 constexpr int BK_DK = 64;          // head dimension of the attention kernels
@@ -163,8 +165,6 @@ hipError_t launch_head_finish(const GemmArgs &g, hipStream_t stream);
 // wavefronts per workgroup of the decode attention (attn_kernel<AW>)
 inline int attn_waves(int M, int H) { return M * H <= 128 ? 8 : 4; }
 hipError_t launch_attn(const AttnArgs &a, hipStream_t stream);
-// k-steps per wavefront the decode GEMM is built for
-constexpr int GEMM_KPW[] = {12, 8, 6, 4, 3, 2};
 hipError_t launch_prefill_attn(const PrefillAttnArgs &a, hipStream_t stream);
 hipError_t launch_embed(const EmbedArgs &a, hipStream_t stream);
 hipError_t launch_rms_rows(const float *x, const float *gamma, float *y, int n, int d, int ld, float eps,

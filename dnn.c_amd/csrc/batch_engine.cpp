@@ -19,13 +19,15 @@
 #include <cstring>
 #include <vector>
 
+#include "engine_plan.h"
 #include "session.h"
 
 using namespace dnnhip;
 
+static_assert(PLAN_MAX_ROWS == MAX_ROWS, "the split-K plans cover every row count of a session");
+
 namespace {
 
-constexpr int CNT_GEMM = 4096;           // last-arriver counters of GEMM column tiles
 constexpr int CNT_ATT = MAX_ROWS * 64;   // (row, head) pairs of the decode attention
 constexpr int CNT_TOTAL = CNT_GEMM + CNT_ATT + 1;
 
@@ -37,42 +39,6 @@ constexpr int CNT_TOTAL = CNT_GEMM + CNT_ATT + 1;
     } while (0)
 
 inline int round_up(int v, int a) { return (v + a - 1) / a * a; }
-
-// Workgroups a decode GEMM without rms_norm is split towards (read once, so
-// the partial buffers sized at engine creation match every launch);
-// DNN_HIP_KS_FILL overrides.  Measured at 32 rows (C3): 64 -> 66.1k tokens/s,
-// 128 / 192 / 256 / 384 -> 64.4k / 64.3k / 63.8k / 63.2k (out_proj split over
-// 2..4 workgroups per tile); 8 rows: 192 0.6% slower; 64 rows within noise.
-int ks_fill() {
-    static const int v = [] {
-        const char *e = getenv("DNN_HIP_KS_FILL");
-        return e ? std::max(1, atoi(e)) : 64;
-    }();
-    return v;
-}
-
-// Split of a decode GEMM: k-steps per wavefront (kpw, one of GEMM_KPW) and
-// workgroups per column tile (ks), K/16 = 4 * ks * kpw.  A wavefront holds all
-// of its A and W loads in registers at once, which bounds kpw by the row tiles
-// per workgroup (mt_max, 0 = all); a GEMM without rms_norm is split further
-// until it has ks_fill() workgroups (the split's partials and last-arriver cost
-// more than the extra parallelism gains below that).
-int pick_ks(int ntiles, int K, int M, bool norm, int mt_max = 0) {
-    const int nks = K / 16, tiles_m = (M + 15) / 16;
-    const int mt = mt_max > 0 && tiles_m > mt_max ? mt_max : tiles_m;
-    const int row_groups = (tiles_m + mt - 1) / mt;
-    static const int lim_norm[4] = {19, 14, 11, 9}, lim_plain[4] = {28, 19, 14, 11};
-    const int lim = (norm ? lim_norm : lim_plain)[mt - 1];
-    int best = 0;
-    for (int kpw : GEMM_KPW) {
-        if (kpw > lim || nks % (4 * kpw)) continue;
-        const int ks = nks / (4 * kpw);
-        if (ks > 8) break;
-        best = ks;
-        if (norm || ntiles * ks * row_groups >= ks_fill()) break;
-    }
-    return best;
-}
 
 // workgroups per (row, head) of the decode attention over histories of up to
 // S_max keys: one where the rows and heads alone fill the chip, else the fewest
@@ -87,64 +53,9 @@ int attn_splits(const dnn_hip_session *s, int M, int H, int S_max) {
     return std::max(1, std::min(8, (nch + 2 * aw - 1) / (2 * aw)));
 }
 
-// Row tiles per workgroup of the decode QKV and gate/up GEMMs (rms_norm fused,
-// not split over K): one for QKV, so every 16 rows launch the column tiles'
-// workgroups again; one for gate/up from 33 rows on, all rows below (measured:
-// 64 rows 149k -> 179k tokens/s with the down GEMM's single tile, 32 rows QKV
-// +0.5%, gate/up at one tile 1% slower).  DNN_HIP_QKV_MT / DNN_HIP_GU_MT
-// override (0: all rows).
-int norm_mt(const char *env, int M, bool qkv) {
-    if (const char *v = getenv(env)) return atoi(v);
-    return qkv || (M + 15) / 16 > 2 ? 1 : 0;
-}
-
-// Row tiles per workgroup of the decode down GEMM (one, as out_proj: 64 rows
-// 160k -> 169k tokens/s, 32 rows unchanged) and lm_head GEMM (all rows: one
-// per workgroup was slower at 32 and 64 rows); DNN_HIP_DOWN_MT /
-// DNN_HIP_HEAD_MT override (0: all rows).
-int plain_mt(const char *env, int dflt) {
-    const char *v = getenv(env);
-    return v ? atoi(v) : dflt;
-}
-
-// Split-K partial pairs a decode GEMM of these dimensions needs.
-size_t part_pairs_for(int N, int K, int M, bool norm, int mt_max = 0) {
-    const int ntn = (N + 15) / 16, ks = pick_ks(ntn, K, M, norm, mt_max);
-    return ks > 1 ? (size_t)ks * M * N + (size_t)ntn * ks * M : 0;
-}
-
-// Row tiles per workgroup (mt_max) of each decode-shape GEMM, as the launches
-// use them: the layer GEMMs of decode steps, and the lm_head of decode steps
-// (head_decode) or of prefill / dnn_hip_head_forward (all rows).
-struct MtPlan {
-    int qkv, out, gu, down, head;
-};
-MtPlan mt_plan(int M, bool head_decode) {
-    MtPlan p;
-    p.qkv = norm_mt("DNN_HIP_QKV_MT", M, true);
-    p.out = 1;                       // out_proj: one 16-row tile per workgroup (more, lighter workgroups)
-    p.gu = norm_mt("DNN_HIP_GU_MT", M, false);
-    p.down = plain_mt("DNN_HIP_DOWN_MT", 1);
-    p.head = head_decode ? plain_mt("DNN_HIP_HEAD_MT", 0) : 0;
-    return p;
-}
-
 // Split-K partial pairs of the engine: the largest need of any decode-shape
 // GEMM launch at any row count (the prefill GEMMs never split K).
-size_t engine_part_pairs(const dnn_hip_model *m) {
-    size_t need = 1;
-    for (int rows = 1; rows <= MAX_ROWS; rows++)
-        for (int hd = 0; hd < 2; hd++) {
-            const MtPlan p = mt_plan(rows, hd != 0);
-            const size_t n[5] = {part_pairs_for(3 * m->D, m->ldD, rows, true, p.qkv),
-                                 part_pairs_for(m->D, m->ldD, rows, false, p.out),
-                                 part_pairs_for(2 * m->F, m->ldD, rows, true, p.gu),
-                                 part_pairs_for(m->D, m->ldF, rows, false, p.down),
-                                 part_pairs_for(m->V, m->ldD, rows, true, p.head)};
-            for (size_t v : n) need = std::max(need, v);
-        }
-    return need;
-}
+size_t engine_part_pairs(const dnn_hip_model *m) { return engine_part_need(m->D, m->F, m->V, m->ldD, m->ldF); }
 
 void free_acts(BatchEngine *e) {
     float *bufs[] = {e->X, e->X1, e->ATT, e->Q, e->ACT};

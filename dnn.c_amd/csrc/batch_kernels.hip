@@ -995,6 +995,7 @@ int prefill_nt(int N, int M) {
 }
 
 // KPW = K / 16 / (4 * ks), chosen by the host among the instantiated values
+// (GEMM_KPW_KW8 / GEMM_KPW_KW4 in engine_plan.h list them)
 template <int EPI, bool NORM, bool BF, int MT>
 hipError_t gemm_decode_mt(const GemmArgs &g, hipStream_t st, int kw, int kpw) {
     const int ntn = (g.N + 15) / 16;
@@ -1019,19 +1020,6 @@ hipError_t gemm_decode_mt(const GemmArgs &g, hipStream_t st, int kw, int kpw) {
     }
 #undef DNNHIP_KPW
     return hipGetLastError();
-}
-
-// Wavefronts splitting K in a decode GEMM workgroup: 8 where each then still
-// holds 2 to 8 k-blocks (half the MFMA chain and loads per wavefront of 4:
-// C3 60.4k -> 61.9k, C5 142k -> 149k tokens/s), else 4; DNN_HIP_GEMM_KW=4
-// keeps 4.
-int decode_kw(int nks, int ks) {
-    static const int forced = [] {
-        const char *e = getenv("DNN_HIP_GEMM_KW");
-        return e ? atoi(e) : 0;
-    }();
-    const bool eight_ok = nks % (8 * ks) == 0 && nks / (8 * ks) >= 2 && nks / (8 * ks) <= 8;
-    return forced != 4 && eight_ok ? 8 : 4;
 }
 
 template <int EPI, bool NORM, bool BF>

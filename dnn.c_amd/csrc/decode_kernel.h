@@ -122,8 +122,9 @@ struct DecodeArgs {
 // -- with every phase's rounds within what a wavefront holds in registers
 // (hold; PE for the down rows) where any split allows that -- the one whose
 // largest per-wavefront weight share of a phase (rounds x unit length) is
-// smallest, then the fewest rounds in total, then the most workgroups.
-// Returns false when G cannot hold one workgroup per role.
+// smallest, then the fewest rounds in total, then the most workgroups; a grid
+// too small for that search splits by weight bytes.  Returns false when G
+// cannot hold one workgroup per role.
 struct Roles {
     int n_ac, n_d, n_e;
 };
@@ -158,7 +159,22 @@ inline bool plan_roles(int G, int D, int F, int ldD, int ldF, int att_records, R
                     out = Roles{nac, nd, ne};
                 }
             }
-    return best_cost >= 0;
+    if (best_cost < 0) {
+        // a grid too small for the searched round counts: workgroups in
+        // proportion to each role's weight bytes, at least one each (the
+        // kernel runs any number of rounds per phase)
+        const double wa = ((double)nuA + nuC) * 2 * ldD, wd = (double)nuD * 2 * ldD, we = (double)nuE * ldF;
+        const double tot = wa + wd + we;
+        int nac = (int)(R * wa / tot), nd = (int)(R * wd / tot);
+        if (nac < 1) nac = 1;
+        if (nd < 1) nd = 1;
+        while (nac + nd > R - 1) {
+            if (nac >= nd && nac > 1) nac--;
+            else nd--;
+        }
+        out = Roles{nac, nd, R - nac - nd};
+    }
+    return true;
 }
 
 // Dynamic LDS of the decode kernel (bytes): per-row token / position / done

@@ -1,0 +1,107 @@
+// CPU check of the launch plans (no GPU call is made).  For model shapes of
+// the BASELINE configs and others, every row count of a session, decode steps
+// and prefill / head calls: each decode-shape GEMM launch the batched engine
+// plans uses an instantiated (wavefronts, k-steps) pair, at most 4 row tiles
+// per workgroup, and split-K partials and counters that fit what the engine
+// allocates for the model (engine_part_need, CNT_GEMM); the persistent
+// kernel's role split is valid for every grid of 4 to 512 workgroups.
+// Prints "plans ok" and exits 0, or names the first failing case.
+#include <cstdio>
+#include <cstdlib>
+
+#include "decode_kernel.h"
+#include "engine_plan.h"
+
+using namespace dnnhip;
+
+static int fails = 0;
+#define CHECK(cond, ...)                        \
+    do {                                        \
+        if (!(cond)) {                          \
+            if (fails++ < 10) {                 \
+                std::printf("FAIL: " __VA_ARGS__); \
+                std::printf("\n");              \
+            }                                   \
+        }                                       \
+    } while (0)
+
+static bool in(const int *a, int n, int v) {
+    for (int i = 0; i < n; i++)
+        if (a[i] == v) return true;
+    return false;
+}
+
+static int round_to(int v, int a) { return (v + a - 1) / a * a; }
+
+static void check_gemm(const char *what, int N, int K, int M, bool norm, int mt_max, size_t part_cap, int D) {
+    const int ntn = (N + 15) / 16, nks = K / 16, tiles_m = (M + 15) / 16;
+    const int ks = pick_ks(ntn, K, M, norm, mt_max);
+    CHECK(ks >= 1, "%s D=%d M=%d: no split fits", what, D, M);
+    if (ks < 1) return;
+    const int kw = decode_kw(nks, ks);
+    CHECK(nks % (kw * ks) == 0, "%s D=%d M=%d: K/16=%d over %d x %d", what, D, M, nks, kw, ks);
+    const int kpw = nks / (kw * ks);
+    const bool inst = kw == 8 ? in(GEMM_KPW_KW8, sizeof GEMM_KPW_KW8 / sizeof(int), kpw)
+                              : in(GEMM_KPW_KW4, sizeof GEMM_KPW_KW4 / sizeof(int), kpw);
+    CHECK(inst, "%s D=%d M=%d: %d wavefronts x %d k-steps not instantiated", what, D, M, kw, kpw);
+    int mt = tiles_m;
+    if (mt_max > 0 && mt > mt_max) mt = mt_max;
+    CHECK(mt >= 1 && mt <= 4, "%s D=%d M=%d: %d row tiles per workgroup", what, D, M, mt);
+    const int groups = (tiles_m + mt - 1) / mt;
+    if (ks > 1) {
+        const size_t need = (size_t)ks * M * N + (size_t)ntn * ks * M;
+        CHECK(need <= part_cap, "%s D=%d M=%d: %zu partial pairs > %zu", what, D, M, need, part_cap);
+        CHECK((size_t)groups * ntn <= (size_t)CNT_GEMM, "%s D=%d M=%d: %d counters > %d", what, D, M, groups * ntn,
+              CNT_GEMM);
+    }
+}
+
+static void check_model(int V, int D, int F) {
+    const int ldD = round_to(D, LDALIGN), ldF = round_to(F, LDALIGN);
+    const size_t cap = engine_part_need(D, F, V, ldD, ldF);
+    for (int M = 1; M <= PLAN_MAX_ROWS; M++)
+        for (int hd = 0; hd < 2; hd++) {
+            const MtPlan p = mt_plan(M, hd != 0);
+            check_gemm("qkv", 3 * D, ldD, M, true, p.qkv, cap, D);
+            check_gemm("out_proj", D, ldD, M, false, p.out, cap, D);
+            check_gemm("gate/up", 2 * F, ldD, M, true, p.gu, cap, D);
+            check_gemm("down", D, ldF, M, false, p.down, cap, D);
+            check_gemm("lm_head", V, ldD, M, true, p.head, cap, D);
+        }
+}
+
+static void check_roles(int D, int F) {
+    const int ldD = round_to(D, LDALIGN), ldF = round_to(F, LDALIGN);
+    const int recs[] = {1, 4, 12, 24, 48, 96};
+    for (int nb : {1, 2, 4, 8})
+        for (int G = 4; G <= 512; G++)
+            for (int r : recs) {
+                Roles ro{};
+                const bool ok = plan_roles(G, D, F, ldD, ldF, r, ro, hold_rounds(nb, ldD / LDALIGN));
+                CHECK(ok, "roles G=%d D=%d records=%d: no split", G, D, r);
+                if (!ok) continue;
+                CHECK(ro.n_ac >= 1 && ro.n_d >= 1 && ro.n_e >= 1 && ro.n_ac + ro.n_d + ro.n_e <= G - 1,
+                      "roles G=%d D=%d records=%d: %d/%d/%d", G, D, r, ro.n_ac, ro.n_d, ro.n_e);
+            }
+}
+
+int main() {
+    // (V, D, F): C1, C2-C4, C5, and other engine shapes (D = 64 * heads <= 768, F <= 2048)
+    const int shapes[][3] = {{128, 256, 683}, {8192, 768, 2048}, {1024, 512, 1024}, {512, 256, 683},
+                             {4096, 384, 1024}, {32000, 640, 1708}, {50257, 768, 2048}, {256, 128, 384},
+                             {1000, 64, 256}, {65535, 768, 2048}};
+    for (const auto &s : shapes) check_model(s[0], s[1], s[2]);
+    // the tests' non-default row tiles
+    setenv("DNN_HIP_QKV_MT", "2", 1);
+    setenv("DNN_HIP_GU_MT", "2", 1);
+    setenv("DNN_HIP_DOWN_MT", "0", 1);
+    setenv("DNN_HIP_HEAD_MT", "1", 1);
+    for (const auto &s : shapes) check_model(s[0], s[1], s[2]);
+    for (const auto &s : shapes) check_roles(s[1], s[2]);
+    if (fails) {
+        std::printf("%d plan checks failed\n", fails);
+        return 1;
+    }
+    std::printf("plans ok\n");
+    return 0;
+}

@@ -193,6 +193,40 @@ def test_session_bounds_are_errors(c1g):
     assert list(s.lengths()) == [0]
 
 
+@pytest.mark.parametrize("grid", [4, 6, 9, 40])
+def test_small_grids_match_default_grid(c1g, grid, monkeypatch):
+    """The persistent kernel on grids down to one workgroup per role (a grid
+    too small for the role planner's search is split by weight bytes, and
+    every phase then runs many rounds): tokens and logits bit-identical to the
+    default grid, since each output's summation order does not depend on how
+    units map to workgroups (one key split, so the attention is the same)."""
+    monkeypatch.setenv("DNN_HIP_ATT_SPLITS", "1")
+    hm = hip_model(c1g)
+    prompt = np.arange(1, 9, dtype=np.int32)
+    ref = A.HipSession(hm, 1, 40)
+    want, wlg = ref.decode(prompt, 24, want_logits=True)
+    s = A.HipSession(hm, 1, 40)
+    s.set_grid(grid)
+    got, glg = s.decode(prompt, 24, want_logits=True)
+    assert s.kernel() == 3 and s.grid() == grid and ref.grid() > 40
+    assert np.array_equal(got, want) and np.array_equal(glg, wlg)
+
+
+def test_small_grid_c2_shape(c2, monkeypatch):
+    """The C2 shape (d=768) on 12 workgroups, below the searched splits (28):
+    the same tokens and logits as the default grid."""
+    monkeypatch.setenv("DNN_HIP_ATT_SPLITS", "1")
+    _, hm = c2
+    prompt = np.arange(3, 9, dtype=np.int32)
+    ref = A.HipSession(hm, 1, 32)
+    want, wlg = ref.decode(prompt, 10, want_logits=True)
+    s = A.HipSession(hm, 1, 32)
+    s.set_grid(12)
+    got, glg = s.decode(prompt, 10, want_logits=True)
+    assert s.grid() == 12
+    assert np.array_equal(got, want) and np.array_equal(glg, wlg)
+
+
 def test_large_batch_is_refused(c1g):
     """Sessions hold at most 64 rows; more is an error at creation."""
     hm = hip_model(c1g)
