@@ -265,11 +265,16 @@ int enqueue_layer(dnn_hip_session *s, int l, const PrefillPlan *pp) {
     const int M = pre ? pp->M : s->B;
     const bool bf = m->bf16 != 0;
     const MtPlan mp = mt_plan(M, true);
+    // GEMM shape: the prefill tiles (128 rows) only for more rows than one
+    // decode-shape launch takes; fewer prefill rows run the decode-shape
+    // GEMMs (16-row tiles, K split over wavefronts and workgroups) like a
+    // decode step of M rows (a 32-token prompt: 3.0 -> 0.5 ms)
+    const bool ps = pre && M > BK_MAXM;
 
     GemmArgs g = gemm_base(s, m->pk_l[(size_t)l * 4 + 0], ldD, 3 * D, ldD);
     g.A = e->X; g.lda = ldD; g.M = M;
-    if (!pre) g.mt_max = mp.qkv;
-    g.ks = pre ? 1 : pick_ks((3 * D + 15) / 16, ldD, M, true, g.mt_max);
+    if (!ps) g.mt_max = mp.qkv;
+    g.ks = ps ? 1 : pick_ks((3 * D + 15) / 16, ldD, M, true, g.mt_max);
     g.part = e->part; g.cnt = e->cnt;
     g.bias = W.f(lo.bqkv);
     g.gamma = W.f(lo.g_attn); g.eps = lo.eps_attn; g.dnorm = D;
@@ -280,7 +285,7 @@ int enqueue_layer(dnn_hip_session *s, int l, const PrefillPlan *pp) {
     g.rope = m->rope; g.rope_rows = m->rope_rows;
     g.kslot = 5 * l;
     g.pk = pk;
-    HIP_TRY(launch_gemm(EPI_QKV, true, bf, pre, g, s->stream));
+    HIP_TRY(launch_gemm(EPI_QKV, true, bf, ps, g, s->stream));
 
     if (pre) {
         PrefillAttnArgs a{};
@@ -304,33 +309,33 @@ int enqueue_layer(dnn_hip_session *s, int l, const PrefillPlan *pp) {
     g.A = e->ATT; g.lda = ldD; g.M = M;
     g.bias = W.f(lo.bo);
     g.out = e->X1; g.ldo = ldD; g.res = e->X; g.ldr = ldD;
-    if (!pre) g.mt_max = mp.out;
-    g.ks = pre ? 1 : pick_ks((D + 15) / 16, ldD, M, false, g.mt_max);
+    if (!ps) g.mt_max = mp.out;
+    g.ks = ps ? 1 : pick_ks((D + 15) / 16, ldD, M, false, g.mt_max);
     g.part = e->part; g.cnt = e->cnt; g.kslot = 5 * l + 2;
     g.pk = pk;
-    HIP_TRY(launch_gemm(EPI_RES, false, bf, pre, g, s->stream));
+    HIP_TRY(launch_gemm(EPI_RES, false, bf, ps, g, s->stream));
 
     g = gemm_base(s, m->pk_l[(size_t)l * 4 + 2], ldD, 2 * m->F, ldD);
     g.A = e->X1; g.lda = ldD; g.M = M;
     g.bias = W.f(lo.bg); g.bias2 = W.f(lo.bu);
     g.gamma = W.f(lo.g_ffn); g.eps = lo.eps_ffn; g.dnorm = D;
     g.out = e->ACT; g.ldo = ldF;
-    if (!pre) g.mt_max = mp.gu;
-    g.ks = pre ? 1 : pick_ks((2 * m->F + 15) / 16, ldD, M, true, g.mt_max);
+    if (!ps) g.mt_max = mp.gu;
+    g.ks = ps ? 1 : pick_ks((2 * m->F + 15) / 16, ldD, M, true, g.mt_max);
     g.part = e->part; g.cnt = e->cnt;
     g.kslot = 5 * l + 3;
     g.pk = pk;
-    HIP_TRY(launch_gemm(EPI_SWIGLU, true, bf, pre, g, s->stream));
+    HIP_TRY(launch_gemm(EPI_SWIGLU, true, bf, ps, g, s->stream));
 
     g = gemm_base(s, m->pk_l[(size_t)l * 4 + 3], ldF, D, ldF);
     g.A = e->ACT; g.lda = ldF; g.M = M;
     g.bias = W.f(lo.bd);
     g.out = e->X; g.ldo = ldD; g.res = e->X1; g.ldr = ldD;
-    if (!pre) g.mt_max = mp.down;
-    g.ks = pre ? 1 : pick_ks((D + 15) / 16, ldF, M, false, g.mt_max);
+    if (!ps) g.mt_max = mp.down;
+    g.ks = ps ? 1 : pick_ks((D + 15) / 16, ldF, M, false, g.mt_max);
     g.part = e->part; g.cnt = e->cnt; g.kslot = 5 * l + 4;
     g.pk = pk;
-    HIP_TRY(launch_gemm(EPI_RES, false, bf, pre, g, s->stream));
+    HIP_TRY(launch_gemm(EPI_RES, false, bf, ps, g, s->stream));
     return DNN_HIP_OK;
 }
 
