@@ -1049,12 +1049,9 @@ template <int EPI, bool NORM, bool BF>
 hipError_t gemm_prefill(const GemmArgs &g, hipStream_t st) {
     // 16-column tiles per wavefront (the workgroup covers 32 * NT columns):
     // DNN_HIP_PREFILL_NT=q,r,s fixes them for the QKV, residual and SwiGLU
-    // GEMMs (0: chosen here)
-    static const int *req = [] {
-        static int v[3] = {0, 0, 0};
-        if (const char *e = getenv("DNN_HIP_PREFILL_NT")) sscanf(e, "%d,%d,%d", &v[0], &v[1], &v[2]);
-        return v;
-    }();
+    // GEMMs (0: chosen here); read at every launch, as the row-tile overrides
+    int req[3] = {0, 0, 0};
+    if (const char *e = getenv("DNN_HIP_PREFILL_NT")) sscanf(e, "%d,%d,%d", &req[0], &req[1], &req[2]);
     const int nt = req[EPI] >= 2 && req[EPI] <= 4 ? req[EPI] : prefill_nt(g.N, g.M);
     const int bn = 32 * nt;
     dim3 grid((g.N + bn - 1) / bn * g.ks, (g.M + BK_PBM - 1) / BK_PBM);

@@ -164,6 +164,28 @@ def test_prefill_causal_matches_cached_forward(c1g, B):
         assert [int(nxt[b])] + list(out[:, b]) == list(want[n[b]:]), "row %d decode after prefill" % b
 
 
+@pytest.mark.parametrize("nt", ["4,4,4", "3,3,3", "2,2,2"])
+def test_prefill_tile_widths(c1g, nt, monkeypatch):
+    """Every prefill GEMM tile width (128, 96 or 64 columns, forced for the
+    QKV, residual and SwiGLU GEMMs) gives the oracle's logits at each row's
+    last position.  The c1g GEMMs have 768, 256 and 1,366 columns, so some
+    widths end in a partial tile; 400-odd rows use the prefill shape."""
+    monkeypatch.setenv("DNN_HIP_PREFILL_NT", nt)
+    hm = hip_model(c1g)
+    rng = np.random.default_rng(77)
+    B = 4
+    n = rng.integers(60, 150, size=B).astype(np.int32)
+    ids = rng.integers(0, 128, size=(B, int(n.max()))).astype(np.int32)
+    s = A.HipSession(hm, B, 200)
+    nxt, lg = s.prefill(ids=ids, n_ids=n, want_logits=True)
+    for b in range(B):
+        st = O.State(c1g, 200)
+        h = st.forward(O.embed(c1g, ids[b, : n[b]]))
+        want = O.head(c1g, h[-1:])
+        assert_logits_close(lg[b:b + 1], want, "row %d prefill, tiles %s" % (b, nt))
+        assert nxt[b] == int(np.argmax(want[0]))
+
+
 def test_prefill_c2_long_prompt(golden):
     """C2: a 288-token prompt prefilled at once (five 64-row tiles, 288-key
     causal attention) against the oracle's cached forward."""
