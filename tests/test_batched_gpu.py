@@ -186,6 +186,29 @@ def test_prefill_tile_widths(c1g, nt, monkeypatch):
         assert nxt[b] == int(np.argmax(want[0]))
 
 
+@pytest.mark.parametrize("B,nmax", [(1, 1), (1, 32), (3, 20), (8, 8)])
+def test_short_prefill_on_decode_gemms(c1g, B, nmax):
+    """Prefills of at most 64 rows run the decode-shape GEMMs: the oracle's
+    logits at each row's last position, then the oracle's generation."""
+    hm = hip_model(c1g)
+    rng = np.random.default_rng(300 + B * 7 + nmax)
+    n = rng.integers(1, nmax + 1, size=B).astype(np.int32)
+    assert int(n.sum()) <= 64
+    ids = rng.integers(0, 128, size=(B, int(n.max()))).astype(np.int32)
+    s = A.HipSession(hm, B, 80)
+    nxt, lg = s.prefill(ids=ids, n_ids=n, want_logits=True)
+    for b in range(B):
+        st = O.State(c1g, 80)
+        h = st.forward(O.embed(c1g, ids[b, : n[b]]))
+        want = O.head(c1g, h[-1:])
+        assert_logits_close(lg[b:b + 1], want, "row %d short prefill" % b)
+        assert nxt[b] == int(np.argmax(want[0]))
+    out, _ = s.decode(nxt, 12)
+    for b in range(B):
+        want = c1g.generate(ids[b, : n[b]], 13, eos=-1)
+        assert [int(nxt[b])] + list(out[:, b]) == list(want[n[b]:]), "row %d decode after short prefill" % b
+
+
 def test_prefill_c2_long_prompt(golden):
     """C2: a 288-token prompt prefilled at once (five 64-row tiles, 288-key
     causal attention) against the oracle's cached forward."""
