@@ -850,6 +850,10 @@ __global__ __launch_bounds__(NTHR) void prefill_attn_kernel(const PrefillAttnArg
         }
         if (key0 + 64 < kv_end) load_kv(key0 + 64);
         __syncthreads();
+        // a wavefront whose 16 rows all lie past the tile's rows (a sequence's
+        // last, short tile) has no scores to compute; it still stages its
+        // share of K/V, and the next iteration starts at the barrier above
+        if (16 * w >= nq) continue;
         f4 S[4];
 #pragma unroll
         for (int nt = 0; nt < 4; nt++) S[nt] = f4{0.f, 0.f, 0.f, 0.f};
