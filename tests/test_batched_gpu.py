@@ -277,6 +277,31 @@ def test_bf16_weights_match_rounded_oracle(B):
         assert_logits_close(lg[5:, b], wlg, "row %d" % b)
 
 
+@pytest.mark.parametrize("B,nmax", [(2, 20), (3, 60)])
+def test_bf16_prefill_matches_rounded_oracle(B, nmax):
+    """bf16 weights through the prefill (at most 64 rows: the decode-shape
+    GEMMs; more: the prefill shape) and the decode after it: the oracle's
+    fp32 arithmetic on the same bf16-rounded weights, to the same bar."""
+    m = O.Model(128, 256, 4, 4, 683, 128, seed=13, init="gpt2")
+    m.round_weights_bf16()
+    hm = A.HipModel(m.V, m.D, m.L, m.H, m.F, m.params(), rope=m.rope_tables(), weights=A.WEIGHTS_BF16)
+    rng = np.random.default_rng(500 + B + nmax)
+    n = rng.integers(nmax // 2, nmax + 1, size=B).astype(np.int32)
+    ids = rng.integers(0, 128, size=(B, int(n.max()))).astype(np.int32)
+    s = A.HipSession(hm, B, 100)
+    nxt, lg = s.prefill(ids=ids, n_ids=n, want_logits=True)
+    for b in range(B):
+        st = O.State(m, 100)
+        h = st.forward(O.embed(m, ids[b, : n[b]]))
+        want = O.head(m, h[-1:])
+        assert_logits_close(lg[b:b + 1], want, "row %d bf16 prefill" % b)
+        assert nxt[b] == int(np.argmax(want[0]))
+    out, _ = s.decode(nxt, 10)
+    for b in range(B):
+        want = m.generate(ids[b, : n[b]], 11, eos=-1)
+        assert [int(nxt[b])] + list(out[:, b]) == list(want[n[b]:]), "row %d bf16 decode after prefill" % b
+
+
 def test_prefill_block_head_after_every_row_stopped():
     """An engine decode whose rows all stop at eos leaves the device step state
     marked done (the rest of its graph replays skip their work).  A prefill,
