@@ -304,13 +304,18 @@ __global__ __launch_bounds__(64 * WM * WN * KW) void gemm_kernel(const GemmArgs 
         }
         for (int kb = kb0; kb < kb1; kb += U) {
             f4 a[U][MT], b[U][NT], gm[U];
+            // every load of the iteration in flight before its first MFMA, in
+            // the order of use: the first k-step's (gamma first), then the
+            // second's (the scheduler would otherwise sink the second k-step's
+            // loads to their uses and wait for each round trip in turn)
 #pragma unroll
             for (int u = 0; u < U; u++) {
+                if (NORM) gm[u] = lda4(rg, (unsigned)(((kb + u) * 16 + 4 * q4) * 4));
 #pragma unroll
                 for (int nt = 0; nt < NT; nt++) b[u][nt] = ldw4<BF>(rwp, pb[nt] + (unsigned)((kb + u) * 256));
 #pragma unroll
                 for (int mt = 0; mt < MT; mt++) a[u][mt] = lda4(ra, aoff[mt] + (unsigned)(kb + u) * astep);
-                if (NORM) gm[u] = lda4(rg, (unsigned)(((kb + u) * 16 + 4 * q4) * 4));
+                __builtin_amdgcn_sched_barrier(0);
             }
 #pragma unroll
             for (int u = 0; u < U; u++) kstep(a[u], b[u], gm[u]);
