@@ -862,14 +862,21 @@ __global__ __launch_bounds__(NTHR) void prefill_attn_kernel(const PrefillAttnArg
         f4 S[4];
 #pragma unroll
         for (int nt = 0; nt < 4; nt++) S[nt] = f4{0.f, 0.f, 0.f, 0.f};
+        // each 16-dimension group's K^T values read from LDS together, then
+        // its MFMAs (read one by one, each read's latency stood before an MFMA)
 #pragma unroll
-        for (int s = 0; s < 4; s++)
+        for (int s = 0; s < 4; s++) {
+            float kq[4][4];
 #pragma unroll
-            for (int j = 0; j < 4; j++) {
-                const float av = qf[s][j];
+            for (int j = 0; j < 4; j++)
 #pragma unroll
-                for (int nt = 0; nt < 4; nt++) S[nt] = mfma4(av, Ks[16 * s + 4 * q4 + j][16 * nt + r16], S[nt]);
-            }
+                for (int nt = 0; nt < 4; nt++) kq[j][nt] = Ks[16 * s + 4 * q4 + j][16 * nt + r16];
+            __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+            for (int j = 0; j < 4; j++)
+#pragma unroll
+                for (int nt = 0; nt < 4; nt++) S[nt] = mfma4(qf[s][j], kq[j][nt], S[nt]);
+        }
         float sc[4];
 #pragma unroll
         for (int v = 0; v < 4; v++) {
@@ -909,13 +916,20 @@ __global__ __launch_bounds__(NTHR) void prefill_attn_kernel(const PrefillAttnArg
         __builtin_amdgcn_s_waitcnt(0xc07f);
         __builtin_amdgcn_wave_barrier();
 #pragma unroll
-        for (int s = 0; s < 4; s++)
+        for (int s = 0; s < 4; s++) {
+            float pq[4], vq[4][4];
 #pragma unroll
             for (int j = 0; j < 4; j++) {
-                const float pv = Ps[w][r16][16 * s + 4 * q4 + j];
+                pq[j] = Ps[w][r16][16 * s + 4 * q4 + j];
 #pragma unroll
-                for (int nt = 0; nt < 4; nt++) O[nt] = mfma4(pv, Vs[16 * s + 4 * q4 + j][16 * nt + r16], O[nt]);
+                for (int nt = 0; nt < 4; nt++) vq[j][nt] = Vs[16 * s + 4 * q4 + j][16 * nt + r16];
             }
+            __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+            for (int j = 0; j < 4; j++)
+#pragma unroll
+                for (int nt = 0; nt < 4; nt++) O[nt] = mfma4(pq[j], vq[j][nt], O[nt]);
+        }
         __builtin_amdgcn_wave_barrier();
     }
 #pragma unroll
