@@ -113,8 +113,8 @@ struct AttnArgs {
     StepState *st;
     int kslot;
     int pk;                     // att rows in fragment order (pk_index)
-    int spec;                   // four-wavefront launches: wavefronts w < spec load their first
-                                // chunk before the row's length is known
+    int spec;                   // wavefronts w < spec load their first chunk before the row's
+                                // length is known
 };
 
 // Prefill attention over the new rows of each sequence: logical rows

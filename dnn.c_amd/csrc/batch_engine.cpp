@@ -410,15 +410,17 @@ int engine_decode(dnn_hip_session *s, const int *feed, int n_feed_all, const int
 
     // the decode attention's speculative loads: the leading wavefronts whose
     // first chunk (64 keys of split 0) at least 3/4 of this call's (row, step)
-    // pairs have, at least one
+    // pairs have, at least one (at least four in eight-wavefront launches:
+    // few (row, head) pairs, so keys fetched for nothing cost little)
     {
         int s_max = 0;
         for (int b = 0; b < B; b++) s_max = std::max(s_max, s->h_pos[b] + n_steps);
         const int ns = attn_splits(s, B, m->H, s_max);
         e->att_ns = ns;
         s->att_splits = ns;
-        int spec = 1;
-        for (int w = 1; w < 4; w++) {
+        const int aw = attn_waves(B, m->H);
+        int spec = aw == 8 ? 4 : 1;
+        for (int w = spec; w < aw; w++) {
             const long long keys = 64LL * ns * w;
             long long have = 0;
             for (int b = 0; b < B; b++) {

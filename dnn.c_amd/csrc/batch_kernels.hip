@@ -640,14 +640,13 @@ __global__ __launch_bounds__(64 * AW) void attn_kernel(const AttnArgs a) {
 #pragma unroll
     for (int i = 0; i < 16; i++) qv[i] = a.q[(size_t)m * a.D + h * BK_DK + q4 + 4 * i];
     const int c0 = sp + a.nsplit * w;
-    // Which wavefronts load their first chunk before the row's length is known.
-    // Few (row, head) pairs (AW = 8): wavefronts 0-3, keys 0-255 of a split,
-    // which most rows have -- latency matters more than keys fetched for
-    // nothing.  Many pairs (AW = 4): the launch moves tens of MB of K/V, so only
-    // the a.spec wavefronts whose chunk most of the call's rows and steps have
-    // (chosen by the host from the positions); the others wait for the length
-    // and fetch only chunks that exist.
-    const bool spec = AW == 8 ? w < 4 : w < a.spec;
+    // Which wavefronts load their first chunk before the row's length is known:
+    // the a.spec leading wavefronts, whose chunk most of the call's rows and
+    // steps have (chosen by the host from the positions; with few (row, head)
+    // pairs, AW = 8, at least four -- latency matters more there than keys
+    // fetched for nothing); the others wait for the length and fetch only
+    // chunks that exist.
+    const bool spec = w < a.spec;
     f4 kt[16], vv[16];
     auto load_chunk = [&](int c) {
         const int j0 = 64 * c;
