@@ -1076,7 +1076,8 @@ hipError_t gemm_prefill(const GemmArgs &g, hipStream_t st) {
     if (const char *e = getenv("DNN_HIP_PREFILL_NT")) sscanf(e, "%d,%d,%d", &req[0], &req[1], &req[2]);
     const int nt = req[EPI] >= 2 && req[EPI] <= 4 ? req[EPI] : prefill_nt(g.N, g.M);
     const int bn = 32 * nt;
-    dim3 grid((g.N + bn - 1) / bn * g.ks, (g.M + BK_PBM - 1) / BK_PBM);
+    if (g.ks != 1) return hipErrorInvalidValue;          // the prefill shape does not split K
+    dim3 grid((g.N + bn - 1) / bn, (g.M + BK_PBM - 1) / BK_PBM);
     if (nt == 2)
         hipLaunchKernelGGL((gemm_kernel<4, 2, 2, 2, 1, 0, BF, EPI, NORM>), grid, dim3(NTHR), 0, st, g);
     else if (nt == 3)
