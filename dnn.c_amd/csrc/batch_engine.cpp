@@ -430,6 +430,8 @@ int engine_decode(dnn_hip_session *s, const int *feed, int n_feed_all, const int
             if (4 * have < 3LL * B * n_steps) break;
             spec = w + 1;
         }
+        // DNN_HIP_ATT_SPEC=n fixes the count (tuning), read at every call
+        if (const char *v = getenv("DNN_HIP_ATT_SPEC")) spec = std::max(1, std::min(aw, atoi(v)));
         e->att_spec = spec;
     }
     // the step graph, captured again when a buffer it names or a launch
