@@ -408,31 +408,14 @@ int engine_decode(dnn_hip_session *s, const int *feed, int n_feed_all, const int
         if (rc) return rc;
     }
 
-    // the decode attention's speculative loads: the leading wavefronts whose
-    // first chunk (64 keys of split 0) at least 3/4 of this call's (row, step)
-    // pairs have, at least one (at least four in eight-wavefront launches:
-    // few (row, head) pairs, so keys fetched for nothing cost little)
+    // the decode attention's key splits and speculative first-chunk loads
     {
         int s_max = 0;
         for (int b = 0; b < B; b++) s_max = std::max(s_max, s->h_pos[b] + n_steps);
         const int ns = attn_splits(s, B, m->H, s_max);
         e->att_ns = ns;
         s->att_splits = ns;
-        const int aw = attn_waves(B, m->H);
-        int spec = aw == 8 ? 4 : 1;
-        for (int w = spec; w < aw; w++) {
-            const long long keys = 64LL * ns * w;
-            long long have = 0;
-            for (int b = 0; b < B; b++) {
-                const long long first = keys - s->h_pos[b];      // steps t with h_pos + t + 1 > keys: t >= first
-                have += std::max(0LL, (long long)n_steps - std::max(0LL, first));
-            }
-            if (4 * have < 3LL * B * n_steps) break;
-            spec = w + 1;
-        }
-        // DNN_HIP_ATT_SPEC=n fixes the count (tuning), read at every call
-        if (const char *v = getenv("DNN_HIP_ATT_SPEC")) spec = std::max(1, std::min(aw, atoi(v)));
-        e->att_spec = spec;
+        e->att_spec = attn_spec(attn_waves(B, m->H), ns, B, n_steps, s->h_pos.data());
     }
     // the step graph, captured again when a buffer it names or a launch
     // parameter changed.  DNN_HIP_ENGINE_GRAPH=0 launches the step's kernels

@@ -1,6 +1,7 @@
 // engine_plan.h -- launch planning of the batched engine's decode-shape GEMMs
 // (workgroups per column tile, row tiles per workgroup, wavefronts splitting
-// K) and the split-K buffers they need.  Plain C++ (no HIP): the engine and a
+// K), the split-K buffers they need, and the decode attention's speculative
+// loads.  Plain C++ (no HIP): the engine and a
 // CPU test of the plans include it.  Internal: not part of the public headers.
 #pragma once
 #include <algorithm>
@@ -113,6 +114,29 @@ inline MtPlan mt_plan(int M, bool head_decode) {
 // Split-K partial pairs the engine needs for a model: the largest need of any
 // decode-shape GEMM launch (QKV, out_proj, gate/up, down, lm_head) at any row
 // count, for decode steps and for prefill / head calls.
+// Decode-attention wavefronts (of aw per workgroup, ns key splits per head)
+// that load their first chunk before the row's length is known: the leading
+// ones whose first chunk (64 keys of split 0) at least 3/4 of the call's
+// (row, step) pairs have -- pos[b] is row b's position at the call's first
+// step -- at least one, and at least four of eight (few (row, head) pairs, so
+// keys fetched for nothing cost little).  DNN_HIP_ATT_SPEC=n fixes it (tuning;
+// read at every call).
+inline int attn_spec(int aw, int ns, int B, int n_steps, const int *pos) {
+    int spec = aw == 8 ? 4 : 1;
+    for (int w = spec; w < aw; w++) {
+        const long long keys = 64LL * ns * w;
+        long long have = 0;
+        for (int b = 0; b < B; b++) {
+            const long long first = keys - pos[b];      // steps t with pos + t + 1 > keys: t >= first
+            have += std::max(0LL, (long long)n_steps - std::max(0LL, first));
+        }
+        if (4 * have < 3LL * B * n_steps) break;
+        spec = w + 1;
+    }
+    if (const char *v = getenv("DNN_HIP_ATT_SPEC")) spec = std::max(1, std::min(aw, atoi(v)));
+    return spec;
+}
+
 inline size_t engine_part_need(int D, int F, int V, int ldD, int ldF) {
     size_t need = 1;
     for (int rows = 1; rows <= PLAN_MAX_ROWS; rows++)

@@ -4,7 +4,8 @@
 // plans uses an instantiated (wavefronts, k-steps) pair, at most 4 row tiles
 // per workgroup, and split-K partials and counters that fit what the engine
 // allocates for the model (engine_part_need, CNT_GEMM); the persistent
-// kernel's role split is valid for every grid of 4 to 512 workgroups.
+// kernel's role split is valid for every grid of 4 to 512 workgroups; the
+// decode attention's speculative loads at the decode shapes.
 // Prints "plans ok" and exits 0, or names the first failing case.
 #include <cstdio>
 #include <cstdlib>
@@ -85,7 +86,38 @@ static void check_roles(int D, int F) {
             }
 }
 
+// the decode attention's speculative first-chunk loads at the BASELINE
+// decode shapes (12 heads; the counts the engine measured best or within noise)
+static void check_spec() {
+    int pos[64];
+    for (int b = 0; b < 8; b++) pos[b] = 1024 + b % 64;
+    CHECK(attn_spec(8, 2, 8, 64, pos) == 8, "C4: all eight wavefronts speculative");
+    for (int b = 0; b < 8; b++) pos[b] = 48;
+    CHECK(attn_spec(8, 1, 8, 512, pos) == 4, "C2 at 8 rows from position 48: four (keys >= 256 in 59%%)");
+    for (int b = 0; b < 32; b++) pos[b] = 16 + (48 * b) / 31;
+    CHECK(attn_spec(4, 1, 32, 256, pos) == 2, "C3: two (keys >= 128 in about 66%%)");
+    for (int b = 0; b < 64; b++) pos[b] = 196 + b % 4;
+    CHECK(attn_spec(4, 1, 64, 16, pos) == 4, "C5: all four (every history past 192 keys)");
+    pos[0] = 0;
+    CHECK(attn_spec(4, 1, 1, 1, pos) == 1, "one new row: one");
+    CHECK(attn_spec(8, 1, 1, 1, pos) == 4, "one new row, eight wavefronts: four");
+    // the 3/4 threshold, exactly: a history of S = pos + t + 1 > 64 keys at
+    // 3 of 4 steps (pos 63: t = 1..3) -> speculative; at 2 of 4 (pos 62) not
+    pos[0] = 63;
+    CHECK(attn_spec(4, 1, 1, 4, pos) == 2, "3 of 4 steps past 64 keys: two");
+    pos[0] = 62;
+    CHECK(attn_spec(4, 1, 1, 4, pos) == 1, "2 of 4 steps past 64 keys: one");
+    // two key splits: wavefront w's first chunk starts at key 128 w
+    pos[0] = 600;
+    CHECK(attn_spec(8, 2, 1, 1, pos) == 5, "two splits, 601 keys: five (key 640 is past the history)");
+    setenv("DNN_HIP_ATT_SPEC", "9", 1);
+    CHECK(attn_spec(4, 1, 1, 4, pos) == 4, "override clamped to the wavefronts");
+    unsetenv("DNN_HIP_ATT_SPEC");
+}
+
 int main() {
+    unsetenv("DNN_HIP_ATT_SPEC");
+    check_spec();
     // (V, D, F): C1, C2-C4, C5, and other engine shapes (D = 64 * heads <= 768, F <= 2048)
     const int shapes[][3] = {{128, 256, 683}, {8192, 768, 2048}, {1024, 512, 1024}, {512, 256, 683},
                              {4096, 384, 1024}, {32000, 640, 1708}, {50257, 768, 2048}, {256, 128, 384},
