@@ -162,8 +162,6 @@ __host__ __device__ inline size_t pk_index(int m, int k, int ld) {
 hipError_t launch_pack(const void *W, void *dst, int N, int ld, bool bf16, hipStream_t stream);
 hipError_t launch_gemm(int epi, bool norm, bool bf16, bool prefill, const GemmArgs &g, hipStream_t stream);
 hipError_t launch_head_finish(const GemmArgs &g, hipStream_t stream);
-// wavefronts per workgroup of the decode attention (attn_kernel<AW>)
-inline int attn_waves(int M, int H) { return M * H <= 128 ? 8 : 4; }
 hipError_t launch_attn(const AttnArgs &a, hipStream_t stream);
 hipError_t launch_prefill_attn(const PrefillAttnArgs &a, hipStream_t stream);
 hipError_t launch_embed(const EmbedArgs &a, hipStream_t stream);

@@ -40,18 +40,9 @@ constexpr int CNT_TOTAL = CNT_GEMM + CNT_ATT + 1;
 
 inline int round_up(int v, int a) { return (v + a - 1) / a * a; }
 
-// workgroups per (row, head) of the decode attention over histories of up to
-// S_max keys: one where the rows and heads alone fill the chip, else the fewest
-// that leave each wavefront at most two 64-key chunks (a split's merge -- the
-// partials, the counter and the last arriver's reload -- costs more than a
-// wider launch gains: measured on 8 rows of 32..1087 keys); at most 8.
-// DNN_HIP_ATT_SPLITS overrides.
-int attn_splits(const dnn_hip_session *s, int M, int H, int S_max) {
-    if (s->att_splits_req > 0) return std::min(8, s->att_splits_req);
-    if (M * H >= 256) return 1;
-    const int aw = attn_waves(M, H), nch = (S_max + 63) / 64;
-    return std::max(1, std::min(8, (nch + 2 * aw - 1) / (2 * aw)));
-}
+// workgroups per (row, head) of the decode attention (attn_splits_for;
+// DNN_HIP_ATT_SPLITS, read at session creation, overrides)
+int attn_splits(const dnn_hip_session *s, int M, int H, int S_max) { return attn_splits_for(s->att_splits_req, M, H, S_max); }
 
 // Split-K partial pairs of the engine: the largest need of any decode-shape
 // GEMM launch at any row count (the prefill GEMMs never split K).

@@ -1,7 +1,7 @@
 // engine_plan.h -- launch planning of the batched engine's decode-shape GEMMs
 // (workgroups per column tile, row tiles per workgroup, wavefronts splitting
-// K), the split-K buffers they need, and the decode attention's speculative
-// loads.  Plain C++ (no HIP): the engine and a
+// K), the split-K buffers they need, and the decode attention's wavefronts,
+// key splits and speculative loads.  Plain C++ (no HIP): the engine and a
 // CPU test of the plans include it.  Internal: not part of the public headers.
 #pragma once
 #include <algorithm>
@@ -114,6 +114,23 @@ inline MtPlan mt_plan(int M, bool head_decode) {
 // Split-K partial pairs the engine needs for a model: the largest need of any
 // decode-shape GEMM launch (QKV, out_proj, gate/up, down, lm_head) at any row
 // count, for decode steps and for prefill / head calls.
+// Wavefronts per workgroup of the decode attention (attn_kernel<AW>) for M
+// rows of H heads: eight where there are few (row, head) pairs, else four.
+inline int attn_waves(int M, int H) { return M * H <= 128 ? 8 : 4; }
+
+// Workgroups per (row, head) of the decode attention over histories of up to
+// S_max keys: one where the rows and heads alone fill the chip, else the fewest
+// that leave each wavefront at most two 64-key chunks (a split's merge -- the
+// partials, the counter and the last arriver's reload -- costs more than a
+// wider launch gains: measured on 8 rows of 32..1087 keys); at most 8.  req > 0
+// (DNN_HIP_ATT_SPLITS) fixes it.
+inline int attn_splits_for(int req, int M, int H, int S_max) {
+    if (req > 0) return std::min(8, req);
+    if (M * H >= 256) return 1;
+    const int aw = attn_waves(M, H), nch = (S_max + 63) / 64;
+    return std::max(1, std::min(8, (nch + 2 * aw - 1) / (2 * aw)));
+}
+
 // Decode-attention wavefronts (of aw per workgroup, ns key splits per head)
 // that load their first chunk before the row's length is known: the leading
 // ones whose first chunk (64 keys of split 0) at least 3/4 of the call's

@@ -5,7 +5,8 @@
 // per workgroup, and split-K partials and counters that fit what the engine
 // allocates for the model (engine_part_need, CNT_GEMM); the persistent
 // kernel's role split is valid for every grid of 4 to 512 workgroups; the
-// decode attention's speculative loads at the decode shapes.
+// decode attention's wavefronts, key splits and speculative loads at the
+// decode shapes.
 // Prints "plans ok" and exits 0, or names the first failing case.
 #include <cstdio>
 #include <cstdlib>
@@ -86,6 +87,20 @@ static void check_roles(int D, int F) {
             }
 }
 
+// the decode attention's wavefronts and key splits at the BASELINE decode
+// shapes (12 heads; a sweep of 1-6 splits found these best)
+static void check_splits() {
+    CHECK(attn_waves(8, 12) == 8 && attn_waves(11, 12) == 4 && attn_waves(32, 12) == 4, "wavefronts per workgroup");
+    CHECK(attn_splits_for(0, 8, 12, 1088) == 2, "C4: 8 rows x 12 heads at 1088 keys: two splits");
+    CHECK(attn_splits_for(0, 8, 12, 560) == 1, "C2 at 8 rows, 560 keys: one split");
+    CHECK(attn_splits_for(0, 32, 12, 320) == 1, "C3: 384 (row, head) pairs fill the chip: one split");
+    CHECK(attn_splits_for(0, 64, 8, 215) == 1, "C5: one split");
+    CHECK(attn_splits_for(0, 1, 12, 1 << 20) == 8, "at most eight splits");
+    CHECK(attn_splits_for(0, 1, 12, 1024) == 1 && attn_splits_for(0, 1, 12, 1025) == 2,
+          "one split up to 16 chunks of 64 keys (8 wavefronts x 2), two past it");
+    CHECK(attn_splits_for(3, 32, 12, 320) == 3 && attn_splits_for(12, 8, 12, 64) == 8, "override, at most eight");
+}
+
 // the decode attention's speculative first-chunk loads at the BASELINE
 // decode shapes (12 heads; the counts the engine measured best or within noise)
 static void check_spec() {
@@ -117,6 +132,7 @@ static void check_spec() {
 
 int main() {
     unsetenv("DNN_HIP_ATT_SPEC");
+    check_splits();
     check_spec();
     // (V, D, F): C1, C2-C4, C5, and other engine shapes (D = 64 * heads <= 768, F <= 2048)
     const int shapes[][3] = {{128, 256, 683}, {8192, 768, 2048}, {1024, 512, 1024}, {512, 256, 683},
